@@ -1,0 +1,342 @@
+"""Benchmark of the quantized matrix-product path on one MI355X.
+
+Headline: INT4 group-wise (group 128, fp16 scale +
+fp16 bias, the reference's layout) decode GEMV over one Llama-3-8B layer --
+q 4096x4096, k/v 1024x4096, o 4096x4096, gate/up 14336x4096, down
+4096x14336 -- at M = 1 fp16 token, fp32 accumulation, fp16 out, weights in
+the gfx950 tiled layout.  One step = one pass over the seven matrices (one
+batched launch).  `value` = algorithmic bytes per step / time per step.
+
+Secondary lines (same JSON object, key "secondary"): M = 8 / 32 tokens, the
+Q4_K 4096^2 GEMV, Q3_K / INT2 Llama-3-70B decode shapes
+(configs[4]) and the FP8 prefill GEMMs.
+
+The weight set is replicated so that each step reads a copy that is not in
+the 256 MB MALL (Infinity Cache) from the previous steps.
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "titan-engine_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+LLAMA8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+           ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+LLAMA70B = [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)]
+ROTATE_BYTES = 768 << 20  # > 3x the 256 MB MALL
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- synthetic weights
+def quant_affine_torch(W, gs, bits):
+    """convert_titan.py:43-77 recipe on the GPU (fp32 min/max, RNE codes,
+    fp16 scale/bias; column 8j+n in nibble n of word j)."""
+    import torch
+    N, K = W.shape
+    levels = (1 << bits) - 1
+    G = W.view(N, K // gs, gs)
+    mn = G.amin(-1)
+    sc = ((G.amax(-1) - mn) / levels).clamp(min=1e-10)
+    q = ((G - mn[..., None]) / sc[..., None]).round().clamp(0, levels).to(torch.int64)
+    per = 32 // bits
+    q = q.view(N, K // per, per)
+    sh = torch.arange(per, device=W.device, dtype=torch.int64) * bits
+    packed = (q << sh).sum(-1)
+    packed = torch.where(packed >= 2 ** 31, packed - 2 ** 32, packed).to(torch.int32)
+    return packed, sc.half(), mn.half()
+
+
+def make_int4_layer(gen, gs=128, bits=4, shapes=LLAMA8B):
+    import numpy as np
+    import torch
+    import titan_qmm as tq
+    fmt = tq.INT4 if bits == 4 else tq.INT2
+    out = []
+    for name, n, k in shapes:
+        W = torch.randn(n, k, generator=gen, device="cuda") * 0.02
+        w, s, b = quant_affine_torch(W, gs, bits)
+        del W
+        t = tq.repack_host(fmt, n, k, w.cpu().numpy(), s.cpu().numpy().view(np.uint16),
+                           b.cpu().numpy().view(np.uint16), gs)
+        out.append(dict(name=name, rows=n, cols=k, fmt=fmt, gs=gs, tiled=torch.from_numpy(t).cuda(),
+                        ref=(w, s, b)))
+    return out
+
+
+def random_kquant(fmt, n, k, gen):
+    """Synthetic Q4_K / Q3_K bytes: random codes, valid fp16 d/dmin of the
+    size N(0, 0.02) weights produce, random 6-bit sub-scales."""
+    import numpy as np
+    import torch
+    import titan_qmm as tq
+    nb = k // 256
+    bb = 144 if fmt == tq.Q4_K else 110
+    blk = torch.randint(0, 256, (n, nb, bb), generator=gen, device="cuda", dtype=torch.int32)
+    blk = blk.to(torch.uint8).cpu().numpy()
+    d = np.float16(0.06 / 63 if fmt == tq.Q4_K else 0.06 / 31 / 4).view(np.uint8)
+    if fmt == tq.Q4_K:
+        blk[:, :, 0:2] = d
+        blk[:, :, 2:4] = d
+    else:
+        blk[:, :, 108:110] = d
+    return blk.reshape(n, nb * bb)
+
+
+# ---------------------------------------------------------------- timing helpers
+def time_launches(fn, steps, warmup):
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        fn(warmup + i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps  # ms per call
+
+
+def copies_for(nbytes):
+    return max(2, min(64, -(-ROTATE_BYTES // max(nbytes, 1))))
+
+
+# ---------------------------------------------------------------- headline
+def bench_int4_layer(M, steps, warmup, gen):
+    import torch
+    import titan_qmm as tq
+    layer = make_int4_layer(gen)
+    wbytes = sum(m["tiled"].numel() for m in layer)
+    R = copies_for(wbytes)
+    copies = [layer] + [[dict(m, tiled=m["tiled"].clone()) for m in layer] for _ in range(R - 1)]
+    Ws = [[tq.QWeight(m["fmt"], tq.LAYOUT_TILED, m["rows"], m["cols"], m["tiled"], group_size=m["gs"])
+           for m in c] for c in copies]
+    X = {k: torch.randn(M, k, generator=gen, device="cuda").half() for k in (4096, 14336)}
+    Xs = [X[m["cols"]] for m in layer]
+    Ys = [torch.empty(M, m["rows"], device="cuda", dtype=torch.float16) for m in layer]
+    abytes = sum(M * m["cols"] * 2 + M * m["rows"] * 2 for m in layer)
+    ms = time_launches(lambda i: tq.qgemm_batched(Ws[i % R], Xs, Ys), steps, warmup)
+    total = wbytes + abytes
+    return dict(ms=ms, bytes=total, wbytes=wbytes, gbs=total / ms / 1e6, copies=R,
+                layer=layer, flops=2 * M * sum(m["rows"] * m["cols"] for m in layer))
+
+
+def bench_single(W_list, x, y, steps, warmup, algo_bytes):
+    import titan_qmm as tq
+    R = len(W_list)
+    ms = time_launches(lambda i: tq.qgemm(W_list[i % R], x, out=y), steps, warmup)
+    return ms, algo_bytes / ms / 1e6
+
+
+def bench_kquant(fmt, n, k, M, gen, steps, warmup):
+    import torch
+    import titan_qmm as tq
+    blk = random_kquant(fmt, n, k, gen)
+    t = tq.repack_host(fmt, n, k, blk)
+    dev = torch.from_numpy(t).cuda()
+    R = copies_for(dev.numel())
+    Wl = [tq.QWeight(fmt, tq.LAYOUT_TILED, n, k, dev if i == 0 else dev.clone()) for i in range(R)]
+    x = torch.randn(M, k, generator=gen, device="cuda").half()
+    y = torch.empty(M, n, device="cuda", dtype=torch.float16)
+    algo = dev.numel() + M * k * 2 + M * n * 2
+    ms, gbs = bench_single(Wl, x, y, steps, warmup, algo)
+    del Wl, dev
+    return dict(ms=ms, gbs=gbs, bytes=algo)
+
+
+def bench_int2(n, k, M, gen, steps, warmup):
+    import torch
+    import titan_qmm as tq
+    (m,) = make_int4_layer(gen, gs=64, bits=2, shapes=[("w", n, k)])
+    R = copies_for(m["tiled"].numel())
+    Wl = [tq.QWeight(tq.INT2, tq.LAYOUT_TILED, n, k, m["tiled"] if i == 0 else m["tiled"].clone(),
+                     group_size=64) for i in range(R)]
+    x = torch.randn(M, k, generator=gen, device="cuda").half()
+    y = torch.empty(M, n, device="cuda", dtype=torch.float16)
+    algo = m["tiled"].numel() + M * k * 2 + M * n * 2
+    ms, gbs = bench_single(Wl, x, y, steps, warmup, algo)
+    return dict(ms=ms, gbs=gbs, bytes=algo)
+
+
+def bench_fp8(M, N, K, gen, steps, warmup):
+    import torch
+    import titan_qmm as tq
+    x = torch.randn(M, K, generator=gen, device="cuda").to(torch.bfloat16)
+    W = torch.randn(N, K, generator=gen, device="cuda") * 0.02
+    sw = (W.abs().amax(1) / 448.0).float()
+    wq = (W / sw[:, None]).to(torch.float8_e4m3fn).view(torch.uint8).contiguous()
+    del W
+    xq = torch.empty(M, K, dtype=torch.uint8, device="cuda")
+    xs = torch.empty(M, device="cuda")
+    out = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+
+    def step(i):
+        tq.fp8_quantize_rows(x, xq, xs)
+        tq.fp8_gemm(xq, xs, wq, sw, out)
+
+    ms = time_launches(step, steps, warmup)
+    gemm_ms = time_launches(lambda i: tq.fp8_gemm(xq, xs, wq, sw, out), steps, warmup)
+    fl = 2.0 * M * N * K
+    return dict(ms=ms, tflops=fl / ms / 1e9, gemm_ms=gemm_ms, gemm_tflops=fl / gemm_ms / 1e9)
+
+
+# ---------------------------------------------------------------- CPU baseline
+def cpu_baseline(layer, budget_s=12.0):
+    """The reference's own AVX-512 CPU expert-path GEMV (matmul_avx.cpp:54-100,
+    built from the reference sources into oracle/_ref) over the same INT4
+    layer, one thread as in the reference, repeated for a bounded sample."""
+    import numpy as np
+    from oracle import oracle_ctypes as O
+    R = O.ref_lib()
+    host = []
+    for m in layer:
+        w, s, b = m["ref"]
+        host.append((w.cpu().numpy().view(np.uint32), s.cpu().numpy().view(np.uint16),
+                     b.cpu().numpy().view(np.uint16), m["rows"], m["cols"]))
+    xs = {k: np.random.default_rng(0).normal(0, 1, k).astype(np.float32) for k in (4096, 14336)}
+    nbytes = sum(m["tiled"].numel() + m["cols"] * 2 + m["rows"] * 2 for m in layer)
+    kind = "reference" if R is not None else "port"
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        for w, s, b, n, k in host:
+            if R is not None:
+                O.ref_matvec_int4(w, s, b, xs[k], n, k, 128)
+            else:
+                O.matvec_int4_cpu(w, s, b, xs[k], n, k, 128)
+        passes += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or passes >= 50:
+            break
+    res = dict(value=round(nbytes * passes / el / 1e9, 3), unit="GB/s", cores=1, kind=kind,
+               sample=f"{passes} pass(es) of the 7-matrix Llama-3-8B INT4 g128 layer, M=1 fp32 x, "
+                      f"{el:.1f} s, {'AVX-512' if R is not None and R.variant == 'avx512' else 'scalar'} "
+                      f"build of matmul_avx.cpp, 1 thread")
+    # the same loop shape over all host cores (row-partitioned restatement)
+    nth = min(os.cpu_count() or 1, 64)
+    t0 = time.perf_counter()
+    mt_passes = 0
+    while True:
+        for w, s, b, n, k in host:
+            O.lib().or_matvec_int4_cpu_mt(*[O._p(a) for a in (w, s, b, xs[k])],
+                                          O._p(np.zeros(n, np.float32)), n, k, 128, nth)
+        mt_passes += 1
+        el = time.perf_counter() - t0
+        if el > budget_s / 2 or mt_passes >= 200:
+            break
+    mt = dict(value=round(nbytes * mt_passes / el / 1e9, 3), unit="GB/s", cores=nth, kind="port",
+              sample=f"{mt_passes} pass(es), rows partitioned over {nth} pthreads")
+    return res, mt
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+# ---------------------------------------------------------------- main
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--headline-only", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import titan_qmm as tq
+    tq.lib()
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    K, W = args.steps, args.warmup
+
+    log("headline: INT4 g128 Llama-3-8B layer, M=1")
+    h = bench_int4_layer(1, K, W, gen)
+    secondary = []
+    if not args.headline_only:
+        for M in (8, 32):
+            r = bench_int4_layer(M, max(20, K // 4), 5, gen)
+            secondary.append(dict(config="INT4 g128 Llama-3-8B layer", M=M, ms=round(r["ms"], 4),
+                                  GBps=round(r["gbs"], 1), frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4),
+                                  TFLOPS=round(r["flops"] / r["ms"] / 1e9, 2)))
+            del r
+        log("Q4_K 4096x4096")
+        r = bench_kquant(tq.Q4_K, 4096, 4096, 1, gen, K, W)
+        secondary.append(dict(config="Q4_K 4096x4096 GEMV (synthetic codes)", M=1,
+                              ms=round(r["ms"], 5), GBps=round(r["gbs"], 1),
+                              frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4)))
+        for M in (1, 4):
+            for n, k in LLAMA70B:
+                log(f"Q3_K / INT2 {n}x{k} M={M}")
+                r = bench_kquant(tq.Q3_K, n, k, M, gen, max(20, K // 2), 5)
+                secondary.append(dict(config=f"Q3_K {n}x{k} GEMV (synthetic codes)", M=M,
+                                      ms=round(r["ms"], 5), GBps=round(r["gbs"], 1),
+                                      frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4)))
+                r = bench_int2(n, k, M, gen, max(20, K // 2), 5)
+                secondary.append(dict(config=f"INT2 g64 {n}x{k} GEMV", M=M, ms=round(r["ms"], 5),
+                                      GBps=round(r["gbs"], 1),
+                                      frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4)))
+                torch.cuda.empty_cache()
+        for (M, N, Kd) in [(2048, 14336, 4096), (2048, 4096, 14336)]:
+            log(f"FP8 GEMM {M}x{N}x{Kd}")
+            r = bench_fp8(M, N, Kd, gen, max(10, K // 10), 3)
+            secondary.append(dict(config=f"FP8 E4M3 GEMM M={M} N={N} K={Kd} (+act quant)",
+                                  ms=round(r["ms"], 4), TFLOPS=round(r["tflops"], 1),
+                                  gemm_only_TFLOPS=round(r["gemm_tflops"], 1),
+                                  frac_fp8_peak=round(r["gemm_tflops"] / FP8_PEAK_TFLOPS, 4)))
+
+    cpu, cpu_mt = (None, None)
+    if not args.no_cpu:
+        log("cpu baseline")
+        cpu, cpu_mt = cpu_baseline(h["layer"])
+        cpu["cpu_model"] = cpu_model()
+
+    line = {
+        "metric": "Q4_K/INT4 decode GEMV GB/s (% of HBM peak); FP8/FP4 GEMM TFLOPS (% peak)",
+        "value": round(h["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(h["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 codes, fp16 scale/bias, fp16 x, fp32 accumulate",
+        "data": "synthetic: weights N(0,0.02) quantized on the GPU with the convert_titan.py "
+                "INT4 recipe; x ~ N(0,1) fp16",
+        "config": {"workload": "INT4 g128 dequant-GEMV, one Llama-3-8B layer (q,k,v,o,gate,up,down), "
+                               "M=1, tiled layout, one batched launch per step",
+                   "algorithmic_bytes_per_step": h["bytes"], "weight_bytes": h["wbytes"],
+                   "weight_copies_rotated": h["copies"]},
+        "roofline": {"bound": "hbm", "achieved": round(h["gbs"], 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(h["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "cpu_baseline_all_cores": cpu_mt,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,180 @@
+"""GPU parity of the dequant and dequant-GEMV kernels against the CPU oracle.
+
+Dequantized values: bit-exact (memcmp of fp32 bits).  Matmul outputs: max
+error normalised by max|ref| <= 1e-3, where ref is the fp64 product of the
+oracle's exact dequantized weights and the activations as rounded to their
+input dtype; fp16/bf16 outputs may also differ from the rounded reference by
+one unit in the last place (helpers.assert_close_out).
+"""
+import numpy as np
+import pytest
+import torch
+
+import titan_qmm as tq
+from helpers import assert_close_out, make_weights, max_rel_err
+from gpu_util import FMTS, TDT, act, dev, to_np, upload
+
+from oracle import oracle_ctypes as O
+
+pytestmark = pytest.mark.gpu
+
+LAYOUTS = {"ref": tq.LAYOUT_REF, "tiled": tq.LAYOUT_TILED}
+SHAPES = {"int4": (64, 1024, 128), "int2": (48, 2048, 64), "fp4": (32, 1024, 64),
+          "nvfp4": (48, 1024, 16), "q4k": (32, 1024, 256), "q3k": (32, 1024, 256),
+          "fp8": (32, 512, 0)}
+
+
+def layouts_for(fmt):
+    return ["ref", "tiled"]
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+@pytest.mark.parametrize("lay", list(LAYOUTS))
+def test_dequant_bit_exact(fmt, lay, rng):
+    rows, cols, gs = SHAPES[fmt]
+    d = make_weights(fmt, rows, cols, rng, gs=gs or 128)
+    W = upload(d, LAYOUTS[lay])
+    out = tq.qdequant(W, torch.float32)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), d["deq"].view(np.uint32))
+    # fp16 / bf16 outputs are the RNE rounding of the exact value
+    h = tq.qdequant(W, torch.float16).cpu()
+    assert torch.equal(h, torch.from_numpy(d["deq"]).to(torch.float16))
+    b = tq.qdequant(W, torch.bfloat16).cpu()
+    assert torch.equal(b, torch.from_numpy(d["deq"]).to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+@pytest.mark.parametrize("lay", list(LAYOUTS))
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 11])
+def test_qgemm_parity(fmt, lay, M, rng):
+    rows, cols, gs = SHAPES[fmt]
+    d = make_weights(fmt, rows, cols, rng, gs=gs or 128)
+    W = upload(d, LAYOUTS[lay])
+    for xdt, ydt in [("f16", "f16"), ("f32", "f32"), ("bf16", "bf16"), ("f16", "f32")]:
+        x, x64 = act(M, cols, xdt, rng)
+        y = tq.qgemm(W, x, out_dtype=TDT[ydt])
+        torch.cuda.synchronize()
+        ref = x64 @ d["deq"].astype(np.float64).T
+        assert_close_out(to_np(y), ref, ydt)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int2", "fp4", "nvfp4", "q4k", "fp8"])
+def test_ragged_rows_and_strides(fmt, rng):
+    # rows not a multiple of 16; x / y with padded row strides
+    rows, cols, gs = {"int4": (37, 512, 64), "int2": (21, 512, 64), "fp4": (19, 256, 32),
+                      "nvfp4": (45, 512, 16), "q4k": (7, 512, 256), "fp8": (29, 256, 0)}[fmt]
+    d = make_weights(fmt, rows, cols, rng, gs=gs or 128)
+    W = upload(d, tq.LAYOUT_REF)
+    xfull = torch.randn(3, cols + 40, dtype=torch.float16, device="cuda")
+    x = xfull[:, :cols]
+    yfull = torch.zeros(3, rows + 24, dtype=torch.float32, device="cuda")
+    y = yfull[:, :rows]
+    tq.qgemm(W, x, out=y)
+    torch.cuda.synchronize()
+    ref = x.double().cpu().numpy() @ d["deq"].astype(np.float64).T
+    assert_close_out(to_np(y), ref, "f32")
+    assert torch.all(yfull[:, rows:] == 0)
+
+
+@pytest.mark.parametrize("fmt,rows,cols,gs", [("int4", 24, 136, 8), ("int4", 16, 200, 40),
+                                              ("int2", 9, 272, 16), ("fp4", 5, 104, 8),
+                                              ("nvfp4", 17, 48, 16), ("q3k", 5, 512, 256)])
+def test_generic_path_odd_shapes(fmt, rows, cols, gs, rng):
+    """Shapes the reference wrappers accept but the 16-byte-slot kernel does
+    not (cols % 32, small groups, Q3_K's 110-byte blocks) take the generic
+    kernel; results must still match."""
+    d = make_weights(fmt, rows, cols, rng, gs=gs)
+    W = upload(d, tq.LAYOUT_REF)
+    x, x64 = act(2, cols, "f32", rng)
+    y = tq.qgemm(W, x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close_out(to_np(y), x64 @ d["deq"].astype(np.float64).T, "f32")
+    out = tq.qdequant(W, torch.float32).cpu().numpy()
+    assert np.array_equal(out.view(np.uint32), d["deq"].view(np.uint32))
+
+
+def test_reference_signature_entry_points(rng):
+    """dispatch.h-shaped calls: fp32 in / fp32 out, REF layout."""
+    rows, cols = 96, 2048
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    xd = dev(x)
+    y = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    # INT4, group 64 (convert_titan.py default) and 128; against the
+    # reference-loop CPU GEMV (matmul_avx.cpp restated, bit-exact with it)
+    for gs in (64, 128):
+        d = make_weights("int4", rows, cols, rng, gs=gs)
+        tq.dequant_matvec_int4(dev(d["codes"]), dev(d["scales"]), dev(d["biases"]), xd, y,
+                               rows, cols, gs)
+        torch.cuda.synchronize()
+        ref = O.matvec_int4_cpu(d["codes"], d["scales"], d["biases"], x, rows, cols, gs)
+        assert max_rel_err(y.cpu().numpy(), ref) < 1e-5
+    d = make_weights("int2", rows, cols, rng, gs=64)
+    tq.dequant_matvec_int2(dev(d["codes"]), dev(d["scales"]), dev(d["biases"]), xd, y, rows,
+                           cols, 64)
+    torch.cuda.synchronize()
+    assert max_rel_err(y.cpu().numpy(), O.gemm_f64(d["deq"], x)[0]) < 1e-5
+    d = make_weights("fp4", rows, cols, rng, gs=32)
+    tq.dequant_matvec_fp4(dev(d["codes"]), dev(d["scales"]), xd, y, rows, cols, 32)
+    torch.cuda.synchronize()
+    assert max_rel_err(y.cpu().numpy(), O.gemm_f64(d["deq"], x)[0]) < 1e-5
+    d = make_weights("nvfp4", rows, cols, rng)
+    tq.dequant_matvec_nvfp4(dev(d["codes"]), dev(d["scales"]), d["g"], xd, y, rows, cols)
+    torch.cuda.synchronize()
+    ref = O.matvec_nvfp4(d["codes"], d["scales"], d["g"], x, rows, cols)  # fp4.cu loop order
+    assert max_rel_err(y.cpu().numpy(), ref) < 1e-5
+
+
+def test_invalid_arguments_launch_nothing():
+    L = tq.lib()
+    y = torch.zeros(16, device="cuda")
+    # cols not a multiple of 8 / of the group size: the reference preconditions
+    st = L.titan_dequant_matvec_int4(None, None, None, None, None, 16, 100, 64, None)
+    assert st == tq.ERR_INVALID_ARG
+    w = torch.zeros(16 * 12, dtype=torch.int32, device="cuda")
+    s = torch.zeros(16 * 2, dtype=torch.float16, device="cuda")
+    x = torch.zeros(100, device="cuda")
+    st = L.titan_dequant_matvec_int4(tq._ptr(w), tq._ptr(s), tq._ptr(s), tq._ptr(x), tq._ptr(y),
+                                     16, 100, 64, None)
+    assert st == tq.ERR_UNSUPPORTED
+    torch.cuda.synchronize()
+    assert torch.all(y == 0)
+
+
+@pytest.mark.parametrize("lay", list(LAYOUTS))
+def test_special_cases(lay, rng):
+    rows, cols, gs = 32, 512, 64
+    # all-zero codes with s = 0, b = 1 -> every weight is 1: y = sum(x)
+    codes = np.zeros((rows, cols // 8), np.uint32)
+    s = np.zeros((rows, cols // gs), np.uint16)
+    b = np.full((rows, cols // gs), 0x3C00, np.uint16)
+    d = {"fmt": "int4", "rows": rows, "cols": cols, "gs": gs, "g": 1.0, "codes": codes,
+         "scales": s, "biases": b}
+    W = upload(d, LAYOUTS[lay])
+    x, x64 = act(1, cols, "f32", rng)
+    y = to_np(tq.qgemm(W, x, out_dtype=torch.float32))
+    assert np.abs(y - x64.sum()).max() < 1e-4
+    # one-hot x returns a dequantized column exactly
+    d = make_weights("q4k", rows, cols, rng)
+    W = upload(d, LAYOUTS[lay])
+    for c in (0, 37, 255, 300, 511):
+        x = torch.zeros(1, cols, device="cuda")
+        x[0, c] = 1.0
+        y = tq.qgemm(W, x, out_dtype=torch.float32).cpu().numpy()[0]
+        assert np.array_equal(y, d["deq"][:, c])
+
+
+@pytest.mark.parametrize("lay", list(LAYOUTS))
+def test_batched_launch_matches_single(lay, rng):
+    shapes = [(64, 1024), (16, 1024), (48, 2048), (32, 512)]
+    ds = [make_weights("int4", r, c, rng, gs=128) for r, c in shapes]
+    Ws = [upload(d, LAYOUTS[lay]) for d in ds]
+    for M in (1, 3):
+        Xs = [torch.randn(M, c, dtype=torch.float16, device="cuda") for _, c in shapes]
+        Ys = [torch.zeros(M, r, dtype=torch.float16, device="cuda") for r, _ in shapes]
+        tq.qgemm_batched(Ws, Xs, Ys)
+        torch.cuda.synchronize()
+        for d, X, Y in zip(ds, Xs, Ys):
+            ref = X.double().cpu().numpy() @ d["deq"].astype(np.float64).T
+            assert_close_out(to_np(Y), ref, "f16")

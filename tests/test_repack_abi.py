@@ -1,0 +1,90 @@
+"""CPU tests of the product library: it loads, exports every symbol that
+include/*.h declares, and its host-side loader repack is an exact byte
+permutation with an exact inverse (no GPU needed for any of these)."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import titan_qmm as tq
+from helpers import make_weights
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FMTS = {"int4": tq.INT4, "int2": tq.INT2, "fp4": tq.FP4, "nvfp4": tq.NVFP4,
+        "q4k": tq.Q4_K, "q3k": tq.Q3_K, "fp8": tq.FP8_E4M3}
+
+
+def declared_functions():
+    names = []
+    inc = os.path.join(ROOT, "include")
+    for f in sorted(os.listdir(inc)):
+        if not f.endswith(".h"):
+            continue
+        text = open(os.path.join(inc, f)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(titan_\w+)\s*\(", text, flags=re.M)
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    L = tq.lib()
+    names = declared_functions()
+    assert len(names) >= 20
+    for n in names:
+        assert hasattr(L, n), n
+    assert L.titan_version().startswith(b"titan-qmm")
+    assert L.titan_status_string(-2) == b"unsupported shape/format/layout"
+
+
+def ref_parts(d):
+    return d["codes"], d["scales"], d["biases"]
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+@pytest.mark.parametrize("rows,cols", [(16, 512), (48, 1024), (32, 2048)])
+def test_repack_roundtrip_bytes(fmt, rows, cols, rng):
+    gs = 64 if fmt in ("int4", "int2", "fp4") else 0
+    d = make_weights(fmt, rows, cols, rng, gs=gs or 128)
+    f = FMTS[fmt]
+    codes, scales, biases = ref_parts(d)
+    if fmt == "fp8":
+        scales = None  # per-row fp32 scales are not part of the tiled buffer
+    n = tq.tiled_bytes(f, rows, cols, gs)
+    ref_bytes = sum(a.nbytes for a in (codes, scales, biases) if a is not None)
+    assert n == ref_bytes, "tiled layout must be a permutation of the REF bytes"
+    t = tq.repack_host(f, rows, cols, codes, scales, biases, gs)
+    c2, s2, b2 = tq.unpack_host(f, rows, cols, t, codes, scales, biases, gs)
+    assert np.array_equal(c2, codes)
+    if scales is not None:
+        assert np.array_equal(s2, scales)
+    if biases is not None:
+        assert np.array_equal(b2, biases)
+    # a permutation: the multiset of bytes is unchanged
+    allref = np.concatenate([np.ascontiguousarray(a).view(np.uint8).ravel()
+                             for a in (codes, scales, biases) if a is not None])
+    assert np.array_equal(np.sort(allref), np.sort(t))
+
+
+def test_repack_code_plane_is_lane_major(rng):
+    d = make_weights("int4", 16, 256, rng, gs=64)
+    t = tq.repack_host(tq.INT4, 16, 256, d["codes"], d["scales"], d["biases"], 64)
+    raw = d["codes"].view(np.uint8).reshape(16, 128)
+    # chunk 0, lane 16*j + r = row r bytes [16j, 16j+16)
+    for j in range(4):
+        for r in range(16):
+            lane = 16 * j + r
+            assert np.array_equal(t[lane * 16:(lane + 1) * 16], raw[r, 16 * j:16 * j + 16])
+    # chunk 1 follows after 1 KiB
+    assert np.array_equal(t[1024:1040], raw[0, 64:80])
+
+
+def test_repack_rejects_untileable_shapes():
+    assert tq.tiled_bytes(tq.INT4, 15, 256, 64) == 0       # rows % 16
+    assert tq.tiled_bytes(tq.INT4, 16, 96, 32) == 0        # 48-byte rows
+    assert tq.tiled_bytes(tq.INT4, 16, 256, 16) == 0       # group inside a 32-col slot
+    assert tq.tiled_bytes(tq.Q4_K, 16, 384, 0) == 0
+    assert tq.tiled_bytes(tq.NVFP4, 16, 128, 0) == 16 * 64 + 16 * 8
+    with pytest.raises(tq.TitanError):
+        tq.repack_host(tq.INT4, 15, 256, np.zeros((15, 32), np.uint32),
+                       np.zeros((15, 4), np.uint16), np.zeros((15, 4), np.uint16), 64)

@@ -1,0 +1,245 @@
+// gemv.hip -- host side of the dequant-GEMV path (validation, batching,
+// C ABI).  Kernels live in gemv_impl.h, instantiated by gemv_fmt_*.hip.
+#include "gemv_impl.h"
+
+// ============================================================================
+// Host side
+// ============================================================================
+namespace {
+
+using namespace tq;
+
+bool fmt_ok(int f) {
+    return f == TITAN_INT4 || f == TITAN_INT2 || f == TITAN_FP4 || f == TITAN_NVFP4 ||
+           f == TITAN_Q4_K || f == TITAN_Q3_K || f == TITAN_FP8_E4M3;
+}
+
+// Validates a weight descriptor against the reference preconditions
+// (dequant.cu / fp4.cu wrappers: cols % 8 (int4, fp4) or % 16 (int2, nvfp4),
+// cols % group_size; K-quants cols % 256).
+int check_weight(const titan_qweight* W) {
+    if (!W || !W->codes || W->rows <= 0 || W->cols <= 0) return TITAN_ERR_INVALID_ARG;
+    if (!fmt_ok(W->format)) return TITAN_ERR_INVALID_ARG;
+    if (W->layout != TITAN_LAYOUT_REF && W->layout != TITAN_LAYOUT_TILED) return TITAN_ERR_INVALID_ARG;
+    const int f = W->format, cols = W->cols, gs = W->group_size;
+    switch (f) {
+        case TITAN_INT4:
+        case TITAN_FP4:
+        case TITAN_INT2:
+            if (gs <= 0 || cols % gs || gs % (f == TITAN_INT2 ? 16 : 8)) return TITAN_ERR_UNSUPPORTED;
+            if (cols % (f == TITAN_INT2 ? 16 : 8)) return TITAN_ERR_UNSUPPORTED;
+            if (W->layout == TITAN_LAYOUT_REF && (!W->scales || (f != TITAN_FP4 && !W->biases)))
+                return TITAN_ERR_INVALID_ARG;
+            break;
+        case TITAN_NVFP4:
+            if (cols % 16) return TITAN_ERR_UNSUPPORTED;
+            if (W->layout == TITAN_LAYOUT_REF && !W->scales) return TITAN_ERR_INVALID_ARG;
+            break;
+        case TITAN_Q4_K:
+        case TITAN_Q3_K:
+            if (cols % 256) return TITAN_ERR_UNSUPPORTED;
+            break;
+        case TITAN_FP8_E4M3:
+            if (!W->scales) return TITAN_ERR_INVALID_ARG;
+            break;
+    }
+    if (W->layout == TITAN_LAYOUT_TILED &&
+        tq::tiled_total_bytes(f, W->rows, cols, gs) == 0)
+        return TITAN_ERR_UNSUPPORTED;
+    return TITAN_OK;
+}
+
+// Can the fast kernel serve this weight?  (Tiled always can.)
+bool fast_ok(const titan_qweight* W) {
+    if (W->layout == TITAN_LAYOUT_TILED) return true;
+    const int f = W->format, cols = W->cols, gs = W->group_size;
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (!al16(W->codes)) return false;
+    switch (f) {
+        case TITAN_INT4: case TITAN_FP4: return cols % 32 == 0 && gs % 32 == 0;
+        case TITAN_INT2: return cols % 64 == 0 && gs % 64 == 0;
+        case TITAN_NVFP4: return cols % 32 == 0 && ((uintptr_t)W->scales & 1) == 0;
+        case TITAN_Q4_K: return true;
+        case TITAN_Q3_K: return false;  // 110-byte blocks: generic path
+        case TITAN_FP8_E4M3: return cols % 16 == 0;
+    }
+    return false;
+}
+
+WDesc make_wdesc(const titan_qweight* W) {
+    WDesc d;
+    d.codes = (const uint8_t*)W->codes;
+    d.scales = (const uint8_t*)W->scales;
+    d.biases = (const uint8_t*)W->biases;
+    d.g = make_geo(W->format, W->rows, W->cols, W->group_size);
+    d.gscale = W->global_scale;
+    return d;
+}
+
+int chunk_cols_of(int fmt) { return 512 / code_bits(fmt); }
+
+// Runs problems [0, n) of one format/layout for tokens [0, M) in launches of
+// at most 8 tokens.
+int run_gemv(const titan_qweight* Ws, const void* const* Xs, const int64_t* ldx,
+             void* const* Ys, const int64_t* ldy, int n, int xdt, int ydt, int M,
+             hipStream_t st) {
+    if (n <= 0 || n > TITAN_MAX_BATCH || M <= 0) return TITAN_ERR_INVALID_ARG;
+    if (!tqh::act_dtype_ok(xdt) || !tqh::act_dtype_ok(ydt)) return TITAN_ERR_INVALID_ARG;
+    bool fast = true;
+    for (int i = 0; i < n; i++) {
+        if (int s = check_weight(&Ws[i])) return s;
+        if (!Xs[i] || !Ys[i]) return TITAN_ERR_INVALID_ARG;
+        if (Ws[i].format != Ws[0].format || Ws[i].layout != Ws[0].layout) return TITAN_ERR_INVALID_ARG;
+        if (ldx[i] < Ws[i].cols || ldy[i] < Ws[i].rows) return TITAN_ERR_INVALID_ARG;
+        fast = fast && fast_ok(&Ws[i]);
+    }
+    const int fmt = Ws[0].format, layout = Ws[0].layout;
+    GemvArgs a{};
+    a.n = n;
+    a.xdt = xdt;
+    a.ydt = ydt;
+    int total_tiles = 0;
+    for (int i = 0; i < n; i++) {
+        GemvProb& p = a.p[i];
+        p.w = make_wdesc(&Ws[i]);
+        p.x = Xs[i];
+        p.y = Ys[i];
+        p.ldx = ldx[i];
+        p.ldy = ldy[i];
+        p.nchunks = (Ws[i].cols + chunk_cols_of(fmt) - 1) / chunk_cols_of(fmt);
+        p.ntiles = (Ws[i].rows + 15) / 16;
+        total_tiles += p.ntiles;
+    }
+    if (!fast) {
+        // the generic kernel serves one problem per launch
+        for (int i = 0; i < n; i++) {
+            GemvArgs one = a;
+            one.p[0] = a.p[i];
+            one.n = 1;
+            for (int m0 = 0; m0 < M; m0 += 8) {
+                one.m0 = m0;
+                int mc = M - m0 < 8 ? M - m0 : 8;
+                switch (fmt) {
+                    case TITAN_INT4: dispatch_gemv_generic_int4(one, mc, Ws[i].rows, st); break;
+                    case TITAN_INT2: dispatch_gemv_generic_int2(one, mc, Ws[i].rows, st); break;
+                    case TITAN_FP4: dispatch_gemv_generic_fp4(one, mc, Ws[i].rows, st); break;
+                    case TITAN_NVFP4: dispatch_gemv_generic_nvfp4(one, mc, Ws[i].rows, st); break;
+                    case TITAN_Q4_K: dispatch_gemv_generic_q4k(one, mc, Ws[i].rows, st); break;
+                    case TITAN_Q3_K: dispatch_gemv_generic_q3k(one, mc, Ws[i].rows, st); break;
+                    default: dispatch_gemv_generic_fp8(one, mc, Ws[i].rows, st); break;
+                }
+            }
+        }
+        return tqh::launch_status();
+    }
+    for (int m0 = 0; m0 < M; m0 += 8) {
+        a.m0 = m0;
+        int mc = M - m0 < 8 ? M - m0 : 8;
+        switch (fmt) {
+            case TITAN_INT4: dispatch_gemv_int4(a, layout, mc, total_tiles, st); break;
+            case TITAN_INT2: dispatch_gemv_int2(a, layout, mc, total_tiles, st); break;
+            case TITAN_FP4: dispatch_gemv_fp4(a, layout, mc, total_tiles, st); break;
+            case TITAN_NVFP4: dispatch_gemv_nvfp4(a, layout, mc, total_tiles, st); break;
+            case TITAN_Q4_K: dispatch_gemv_q4k(a, layout, mc, total_tiles, st); break;
+            case TITAN_Q3_K: dispatch_gemv_q3k(a, layout, mc, total_tiles, st); break;
+            default: dispatch_gemv_fp8(a, layout, mc, total_tiles, st); break;
+        }
+    }
+    return tqh::launch_status();
+}
+
+}  // namespace
+
+// ============================================================================
+// C ABI
+// ============================================================================
+extern "C" int titan_qgemm(const titan_qweight* W, const void* X, int x_dtype, int64_t ldx,
+                           void* Y, int y_dtype, int64_t ldy, int M, hipStream_t stream) {
+    if (!W) return TITAN_ERR_INVALID_ARG;
+    const void* xs[1] = {X};
+    void* ys[1] = {Y};
+    return run_gemv(W, xs, &ldx, ys, &ldy, 1, x_dtype, y_dtype, M, stream);
+}
+
+extern "C" int titan_qgemm_batched(const titan_qweight* Ws, const void* const* Xs,
+                                   void* const* Ys, int n, int x_dtype, int y_dtype, int M,
+                                   hipStream_t stream) {
+    if (!Ws || !Xs || !Ys || n <= 0 || n > TITAN_MAX_BATCH) return TITAN_ERR_INVALID_ARG;
+    int64_t ldx[TITAN_MAX_BATCH], ldy[TITAN_MAX_BATCH];
+    for (int i = 0; i < n; i++) {
+        ldx[i] = Ws[i].cols;
+        ldy[i] = Ws[i].rows;
+    }
+    return run_gemv(Ws, Xs, ldx, Ys, ldy, n, x_dtype, y_dtype, M, stream);
+}
+
+extern "C" int titan_qdequant(const titan_qweight* W, void* out, int out_dtype,
+                              hipStream_t stream) {
+    if (int s = check_weight(W)) return s;
+    if (!out || !tqh::act_dtype_ok(out_dtype)) return TITAN_ERR_INVALID_ARG;
+    WDesc d = make_wdesc(W);
+    int64_t n = (int64_t)W->rows * W->cols;
+    int blocks = (int)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536);
+    bool tiled = W->layout == TITAN_LAYOUT_TILED;
+#define TQ_DQ(FMTV)                                                                               \
+    case FMTV:                                                                                    \
+        if (tiled)                                                                                \
+            hipLaunchKernelGGL((qdequant_kernel<FMTV, TITAN_LAYOUT_TILED>), dim3(blocks), dim3(256), \
+                               0, stream, d, out, out_dtype);                                     \
+        else                                                                                      \
+            hipLaunchKernelGGL((qdequant_kernel<FMTV, TITAN_LAYOUT_REF>), dim3(blocks), dim3(256),   \
+                               0, stream, d, out, out_dtype);                                     \
+        break;
+    switch (W->format) {
+        TQ_DQ(TITAN_INT4)
+        TQ_DQ(TITAN_INT2)
+        TQ_DQ(TITAN_FP4)
+        TQ_DQ(TITAN_NVFP4)
+        TQ_DQ(TITAN_Q4_K)
+        TQ_DQ(TITAN_Q3_K)
+        TQ_DQ(TITAN_FP8_E4M3)
+    }
+#undef TQ_DQ
+    return tqh::launch_status();
+}
+
+// ---- reference-signature entry points (dispatch.h) ------------------------------
+static int ref_matvec(int fmt, const void* w, const void* s, const void* b, float g,
+                      const float* x, float* y, int rows, int cols, int gs, hipStream_t st) {
+    titan_qweight W{};
+    W.format = fmt;
+    W.layout = TITAN_LAYOUT_REF;
+    W.rows = rows;
+    W.cols = cols;
+    W.group_size = gs;
+    W.global_scale = g;
+    W.codes = w;
+    W.scales = s;
+    W.biases = b;
+    return titan_qgemm(&W, x, TITAN_FP32, cols, y, TITAN_FP32, rows, 1, st);
+}
+
+extern "C" int titan_dequant_matvec_int4(const void* weights, const void* scales,
+                                         const void* biases, const float* input, float* output,
+                                         int rows, int cols, int group_size, hipStream_t stream) {
+    return ref_matvec(TITAN_INT4, weights, scales, biases, 1.0f, input, output, rows, cols,
+                      group_size, stream);
+}
+extern "C" int titan_dequant_matvec_int2(const void* weights, const void* scales,
+                                         const void* biases, const float* input, float* output,
+                                         int rows, int cols, int group_size, hipStream_t stream) {
+    return ref_matvec(TITAN_INT2, weights, scales, biases, 1.0f, input, output, rows, cols,
+                      group_size, stream);
+}
+extern "C" int titan_dequant_matvec_fp4(const void* weights, const void* scales, const float* input,
+                                        float* output, int rows, int cols, int group_size,
+                                        hipStream_t stream) {
+    return ref_matvec(TITAN_FP4, weights, scales, nullptr, 1.0f, input, output, rows, cols,
+                      group_size, stream);
+}
+extern "C" int titan_dequant_matvec_nvfp4(const void* weights, const void* scales,
+                                          float global_scale, const float* input, float* output,
+                                          int rows, int cols, hipStream_t stream) {
+    return ref_matvec(TITAN_NVFP4, weights, scales, nullptr, global_scale, input, output, rows,
+                      cols, 16, stream);
+}

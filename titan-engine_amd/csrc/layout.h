@@ -1,0 +1,141 @@
+// layout.h -- geometry of every weight format in both layouts.
+//
+// Shared by the host repack (repack.cpp) and the device kernels so that the
+// two can never disagree about where a byte lives.
+//
+// TILED layout (one buffer, all planes back to back, same byte count as REF):
+//   code plane   row r's code bytes (K-quants: the concatenated qs arrays of
+//                its blocks) cut into 64-byte chunks; tile t = rows 16t..16t+15;
+//                chunk c of tile t is 1 KiB at ((t*nchunks + c) * 64 + lane) * 16
+//                with lane = 16*j + (r % 16) holding bytes [64c + 16j, +16) of
+//                row r.  A wave's 64 lanes read one chunk of 16 rows as 1 KiB
+//                of contiguous memory.
+//   aux planes   per format, also 16-row interleaved (see tiled_* below).
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifndef TQ_HD
+#define TQ_HD __host__ __device__ __forceinline__
+#endif
+
+namespace tq {
+
+struct Geo {
+    int fmt;
+    int rows, cols, gs;
+    int row_code_bytes;  // bytes of the code plane per row
+    int nchunks;         // 64-byte chunks per row (tiled)
+    int chunk_cols;      // columns covered by one 64-byte chunk
+    int slot_cols;       // columns covered by one lane's 16 bytes
+    int nblk;            // K-quant blocks per row
+    int ngroups;         // INT4/INT2/FP4 scale groups per row
+};
+
+TQ_HD int code_bits(int fmt) {
+    switch (fmt) {
+        case TITAN_INT4: case TITAN_FP4: case TITAN_NVFP4: case TITAN_Q4_K: return 4;
+        case TITAN_INT2: case TITAN_Q3_K: return 2;
+        case TITAN_FP8_E4M3: return 8;
+        default: return 0;
+    }
+}
+
+TQ_HD Geo make_geo(int fmt, int rows, int cols, int gs) {
+    Geo g;
+    g.fmt = fmt;
+    g.rows = rows;
+    g.cols = cols;
+    g.gs = gs;
+    int bits = code_bits(fmt);
+    g.row_code_bytes = bits ? (int)(((int64_t)cols * bits) / 8) : 0;
+    g.nchunks = g.row_code_bytes / 64;
+    g.chunk_cols = bits ? 512 / bits : 0;
+    g.slot_cols = bits ? 128 / bits : 0;
+    g.nblk = (fmt == TITAN_Q4_K || fmt == TITAN_Q3_K) ? cols / 256 : 0;
+    g.ngroups = (gs > 0 && (fmt == TITAN_INT4 || fmt == TITAN_INT2 || fmt == TITAN_FP4))
+                    ? cols / gs : 0;
+    return g;
+}
+
+// Bytes per K-quant block in the REF (ggml) layout.
+TQ_HD int kquant_block_bytes(int fmt) { return fmt == TITAN_Q4_K ? 144 : 110; }
+
+// ---- TILED code plane ------------------------------------------------------
+TQ_HD size_t tiled_code_off(const Geo& g, int row, int chunk, int j) {
+    int t = row >> 4, r = row & 15;
+    return (((size_t)t * g.nchunks + chunk) * 64 + (size_t)(j * 16 + r)) * 16;
+}
+TQ_HD size_t tiled_code_plane_bytes(const Geo& g) {
+    return (size_t)g.rows * g.row_code_bytes;
+}
+
+// ---- TILED aux planes (offsets from the start of the buffer) ----------------
+// INT4 / INT2: u32 (scale | bias << 16) at [t][group][r].
+TQ_HD size_t tiled_sb_off(const Geo& g, int row, int grp) {
+    return tiled_code_plane_bytes(g) +
+           (((size_t)(row >> 4) * g.ngroups + grp) * 16 + (row & 15)) * 4;
+}
+// FP4: u16 scale at [t][group][r].
+TQ_HD size_t tiled_fp4s_off(const Geo& g, int row, int grp) {
+    return tiled_code_plane_bytes(g) +
+           (((size_t)(row >> 4) * g.ngroups + grp) * 16 + (row & 15)) * 2;
+}
+// NVFP4: u16 (two e4m3 scales of slot j of chunk c) at [t][c][j][r].
+TQ_HD size_t tiled_nvs_off(const Geo& g, int row, int chunk, int j) {
+    return tiled_code_plane_bytes(g) +
+           ((((size_t)(row >> 4) * g.nchunks + chunk) * 4 + j) * 16 + (row & 15)) * 2;
+}
+// Q4_K: 16-byte block header {d, dmin, scales[12]} at [t][blk][r].
+TQ_HD size_t tiled_q4k_hdr_off(const Geo& g, int row, int blk) {
+    return tiled_code_plane_bytes(g) +
+           (((size_t)(row >> 4) * g.nblk + blk) * 16 + (row & 15)) * 16;
+}
+// Q3_K: hmask halves (16 B) at [t][blk][hh][r]; scales (12 B) at [t][blk][r];
+// d (2 B) at [t][blk][r].
+TQ_HD size_t tiled_q3k_hmask_off(const Geo& g, int row, int blk, int hh) {
+    return tiled_code_plane_bytes(g) +
+           ((((size_t)(row >> 4) * g.nblk + blk) * 2 + hh) * 16 + (row & 15)) * 16;
+}
+TQ_HD size_t tiled_q3k_sc_off(const Geo& g, int row, int blk) {
+    return tiled_code_plane_bytes(g) + (size_t)g.rows * g.nblk * 32 +
+           (((size_t)(row >> 4) * g.nblk + blk) * 16 + (row & 15)) * 12;
+}
+TQ_HD size_t tiled_q3k_d_off(const Geo& g, int row, int blk) {
+    return tiled_code_plane_bytes(g) + (size_t)g.rows * g.nblk * 44 +
+           (((size_t)(row >> 4) * g.nblk + blk) * 16 + (row & 15)) * 2;
+}
+
+// Total bytes of the TILED buffer, or 0 if the format/shape has no tiled
+// form.  Tiled weights are always served by the fast GEMV kernel, so the
+// group size must also keep each lane's 16-byte slot inside one group.
+TQ_HD size_t tiled_total_bytes(int fmt, int rows, int cols, int gs) {
+    if (rows <= 0 || cols <= 0 || (rows & 15)) return 0;
+    Geo g = make_geo(fmt, rows, cols, gs);
+    if (!g.row_code_bytes || (g.row_code_bytes & 63)) return 0;
+    size_t codes = tiled_code_plane_bytes(g);
+    switch (fmt) {
+        case TITAN_INT4:
+        case TITAN_INT2:
+            if (gs <= 0 || cols % gs || gs % g.slot_cols) return 0;
+            return codes + (size_t)rows * g.ngroups * 4;
+        case TITAN_FP4:
+            if (gs <= 0 || cols % gs || gs % g.slot_cols) return 0;
+            return codes + (size_t)rows * g.ngroups * 2;
+        case TITAN_NVFP4:
+            return codes + (size_t)rows * (cols / 16);
+        case TITAN_Q4_K:
+            if (cols % 256) return 0;
+            return codes + (size_t)rows * g.nblk * 16;
+        case TITAN_Q3_K:
+            if (cols % 256) return 0;
+            return codes + (size_t)rows * g.nblk * 46;
+        case TITAN_FP8_E4M3:
+            return codes;
+        default:
+            return 0;
+    }
+}
+
+}  // namespace tq
