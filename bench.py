@@ -83,7 +83,7 @@ def random_kquant(fmt, n, k, gen):
     bb = 144 if fmt == tq.Q4_K else 110
     blk = torch.randint(0, 256, (n, nb, bb), generator=gen, device="cuda", dtype=torch.int32)
     blk = blk.to(torch.uint8).cpu().numpy()
-    d = np.float16(0.06 / 63 if fmt == tq.Q4_K else 0.06 / 31 / 4).view(np.uint8)
+    d = np.array([0.06 / 63 if fmt == tq.Q4_K else 0.06 / 31 / 4], np.float16).view(np.uint8)
     if fmt == tq.Q4_K:
         blk[:, :, 0:2] = d
         blk[:, :, 2:4] = d

@@ -73,6 +73,9 @@ WDesc make_wdesc(const titan_qweight* W) {
     d.biases = (const uint8_t*)W->biases;
     d.g = make_geo(W->format, W->rows, W->cols, W->group_size);
     d.gscale = W->global_scale;
+    d.gshift = -1;
+    for (int sh = 0; sh < 31; sh++)
+        if (W->group_size == (1 << sh)) d.gshift = sh;
     return d;
 }
 
