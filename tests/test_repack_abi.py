@@ -67,16 +67,18 @@ def test_repack_roundtrip_bytes(fmt, rows, cols, rng):
 
 
 def test_repack_code_plane_is_lane_major(rng):
+    """Chunk c of a 16-row tile is 1 KiB in lane order (lane = 16*j + r); lane
+    (r, j) holds words j, 4+j, 8+j, 12+j of row r's 64-byte chunk."""
     d = make_weights("int4", 16, 256, rng, gs=64)
     t = tq.repack_host(tq.INT4, 16, 256, d["codes"], d["scales"], d["biases"], 64)
-    raw = d["codes"].view(np.uint8).reshape(16, 128)
-    # chunk 0, lane 16*j + r = row r bytes [16j, 16j+16)
-    for j in range(4):
-        for r in range(16):
-            lane = 16 * j + r
-            assert np.array_equal(t[lane * 16:(lane + 1) * 16], raw[r, 16 * j:16 * j + 16])
-    # chunk 1 follows after 1 KiB
-    assert np.array_equal(t[1024:1040], raw[0, 64:80])
+    words = d["codes"].reshape(16, 32)  # row -> 32 words (two chunks of 16)
+    tw = t[:16 * 128].view(np.uint32)
+    for c in range(2):
+        for j in range(4):
+            for r in range(16):
+                lane = 16 * j + r
+                got = tw[c * 256 + lane * 4: c * 256 + lane * 4 + 4]
+                assert got.tolist() == [int(words[r, 16 * c + 4 * i + j]) for i in range(4)]
 
 
 def test_repack_rejects_untileable_shapes():
@@ -85,6 +87,7 @@ def test_repack_rejects_untileable_shapes():
     assert tq.tiled_bytes(tq.INT4, 16, 256, 16) == 0       # group inside a 32-col slot
     assert tq.tiled_bytes(tq.Q4_K, 16, 384, 0) == 0
     assert tq.tiled_bytes(tq.NVFP4, 16, 128, 0) == 16 * 64 + 16 * 8
+    assert tq.tiled_bytes(tq.NVFP4, 16, 64, 0) == 0         # NVFP4 tiles whole 128-column chunks
     with pytest.raises(tq.TitanError):
         tq.repack_host(tq.INT4, 15, 256, np.zeros((15, 32), np.uint32),
                        np.zeros((15, 4), np.uint16), np.zeros((15, 4), np.uint16), 64)

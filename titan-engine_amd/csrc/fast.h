@@ -1,0 +1,839 @@
+// fast.h -- the GEMV/small-M GEMM view of each weight format.
+//
+// A wave covers 16 rows x one 64-byte chunk of codes per row.  Lane
+// l = 16*j + r (r = row in the tile, j = 0..3) holds words j, 4+j, 8+j, 12+j
+// of row r's chunk: word i of the lane covers chunk bytes [16i + 4j, +4), so
+// the four lanes of a row together cover chunk bytes [16i, 16i + 16) at "word
+// step" i -- a run of contiguous columns inside one scale group.
+//
+// Three ways to fold a chunk against activations (all fp32 accumulation):
+//  * fold_f32  (fp32 / bf16 activations): codes to fp32, FMA with fp32 x held
+//    in natural column order in LDS.
+//  * fold_h    (fp16 activations): a code word masked to bits inside the fp16
+//    mantissa is a pair of exact fp16 subnormals (code * 2^-24 * 2^shift);
+//    v_dot2_f32_f16 multiplies it with an activation pair.  Activations sit
+//    in LDS permuted per format (stage8) so one 128-bit read yields the
+//    pairs that line up with the masked code pairs.
+//  * fold_mfma (fp16 activations, selected formats): the same fp16 code
+//    operands feed v_mfma_f32_16x16x{16,32}_f16 with activations as the A
+//    operand (16 tokens x k) and codes as B (k x 16 rows); lane (r, q) of the
+//    accumulator holds row r, tokens 4q..4q+3, so the lane's own per-row
+//    scales apply without data movement.  Bias / min terms use the sum of x
+//    over the group, taken by an extra MFMA against a vector of ones.
+// fold_f32 / fold_h return the lane's partial dot product for one token; the
+// four lanes of a row are summed afterwards.  Bias-like terms (scale *
+// sum(x over the group)) are added by lane j == 0 only, with the group's full
+// activation sum from the per-16-column sums staged in LDS.
+#pragma once
+
+#include "formats.h"
+
+namespace tq {
+
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// ---- fp16 helpers -------------------------------------------------------------
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+TQ_DEV h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
+TQ_DEV float dot2(uint32_t codes, uint32_t x2, float acc) {
+    return __builtin_amdgcn_fdot2(as_h2(codes), as_h2(x2), acc, false);
+}
+constexpr float kTwo24 = 16777216.0f;  // 2^24
+constexpr float kTwo14 = 16384.0f;     // 2^14
+constexpr uint32_t kOnes2 = 0x3C003C00u;  // fp16 pair (1, 1)
+
+TQ_DEV h4_t h4_of(uint32_t a, uint32_t b) { return __builtin_bit_cast(h4_t, make_uint2(a, b)); }
+TQ_DEV h8_t h8_of(uint4 v) { return __builtin_bit_cast(h8_t, v); }
+TQ_DEV f4_t mfma16(h4_t a, h4_t b, f4_t c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
+TQ_DEV f4_t mfma32(h8_t a, h8_t b, f4_t c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+TQ_DEV f4_t f4_zero() { return (f4_t){0.f, 0.f, 0.f, 0.f}; }
+
+// E2M1 codes of a word as fp16 pairs (value = lut * 2^-14): nibbles n and
+// n + 4 of word w become the low / high halves of fp4_pair(w, n).
+TQ_DEV uint32_t fp4_pair(uint32_t w, int n) {
+    switch (n) {  // magnitude bits (e1 e0 m) -> fp16 bits 11..9, sign -> bit 15
+        case 0: return ((w & 0x00070007u) << 9) | ((w & 0x00080008u) << 12);
+        case 1: return ((w & 0x00700070u) << 5) | ((w & 0x00800080u) << 8);
+        case 2: return ((w & 0x07000700u) << 1) | ((w & 0x08000800u) << 4);
+        default: return ((w >> 3) & 0x0E000E00u) | (w & 0x80008000u);
+    }
+}
+
+// fp32 dot product of 8 nibbles (column n in bits 4n) with x[0..7]
+TQ_DEV float dot_nib8(uint32_t w, const float* x) {
+    uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    float a = (float)(lo & 0xFF) * x[0];
+    float b = (float)(hi & 0xFF) * x[1];
+    a = __builtin_fmaf((float)((lo >> 8) & 0xFF), x[2], a);
+    b = __builtin_fmaf((float)((hi >> 8) & 0xFF), x[3], b);
+    a = __builtin_fmaf((float)((lo >> 16) & 0xFF), x[4], a);
+    b = __builtin_fmaf((float)((hi >> 16) & 0xFF), x[5], b);
+    a = __builtin_fmaf((float)(lo >> 24), x[6], a);
+    b = __builtin_fmaf((float)(hi >> 24), x[7], b);
+    return a + b;
+}
+TQ_DEV void ld_f8(const float* p, float* x) {
+    float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
+TQ_DEV void ld_f4(const float* p, float* x) {
+    float4 a = *(const float4*)p;
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+}
+
+// Group index of a column: the fast path only takes power-of-two groups.
+TQ_DEV int group_of(const WDesc& w, int col) { return col >> w.gshift; }
+
+// Staging helpers: 8 / 4 fp16 activations from a natural-order row.
+TQ_DEV void ldh8(const _Float16* p, _Float16* h) {
+    uint4 v = *(const uint4*)p;
+    h8_t t = h8_of(v);
+#pragma unroll
+    for (int i = 0; i < 8; i++) h[i] = t[i];
+}
+TQ_DEV void ldh4(const _Float16* p, _Float16* h) {
+    uint2 v = *(const uint2*)p;
+    h4_t t = __builtin_bit_cast(h4_t, v);
+#pragma unroll
+    for (int i = 0; i < 4; i++) h[i] = t[i];
+}
+TQ_DEV uint4 pack8(const _Float16* o) {
+    h8_t t;
+#pragma unroll
+    for (int i = 0; i < 8; i++) t[i] = o[i];
+    return __builtin_bit_cast(uint4, t);
+}
+
+// ============================================================================
+// INT4 affine (dequant.cu:23-104): word (4i+j) = columns 32i + 8j + n of the
+// chunk (nibble n).  Word step i lies in group (128c + 32i) >> gshift.
+// LDS activation order: per 8 columns [0,4,2,6,1,5,3,7].
+// ============================================================================
+template <int LAYOUT, bool IS_FP4 = false>
+struct FxNib {
+    static constexpr int FMT = IS_FP4 ? TITAN_FP4 : TITAN_INT4;
+    static constexpr int CHUNK_COLS = 128;
+    static constexpr bool HAS_MFMA = !IS_FP4;
+    struct Off { uint32_t c, s, b; };
+    struct Raw { uint32_t w[4], s[4], b[4]; };
+    struct Dec { float s[4], b[4]; };
+    TQ_DEV static Off base(const WDesc& w, int row, int j) {
+        const Geo& g = w.g;
+        if constexpr (LAYOUT == TITAN_LAYOUT_REF)
+            return {(uint32_t)row * (uint32_t)g.row_code_bytes + 4u * j,
+                    (uint32_t)row * (uint32_t)(g.ngroups * 2), (uint32_t)row * (uint32_t)(g.ngroups * 2)};
+        else if constexpr (IS_FP4)
+            return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_fp4s_off(g, row, 0), 0u};
+        else
+            return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_sb_off(g, row, 0), 0u};
+    }
+    template <int GS>
+    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
+        if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
+        } else {
+            uint4 q = ld_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
+        }
+#pragma unroll
+        for (int i = GS - 1; i < 4; i += GS) {  // last word step of each group
+            const uint32_t grp = (uint32_t)group_of(w, c * 128 + 32 * i);
+            if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
+                r.s[i] = ld_u16(w.scales + (o.s + grp * 2u));
+                if constexpr (!IS_FP4) r.b[i] = ld_u16(w.biases + (o.b + grp * 2u));
+            } else if constexpr (IS_FP4) {
+                r.s[i] = ld_u16(w.codes + (o.s + grp * 32u));
+            } else {
+                r.s[i] = ld_u32(w.codes + (o.s + grp * 64u));
+            }
+        }
+    }
+    template <int GS>
+    TQ_DEV static Dec decode(const WDesc&, const Raw& r, int, int) {
+        Dec d;  // step i takes the scales loaded for the last step of its group
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int k = i | (GS - 1);
+            if constexpr (LAYOUT == TITAN_LAYOUT_TILED && !IS_FP4) {
+                d.s[i] = f16_to_f32(r.s[k] & 0xFFFF);
+                d.b[i] = f16_to_f32(r.s[k] >> 16);
+            } else {
+                d.s[i] = f16_to_f32(r.s[k]);
+                d.b[i] = IS_FP4 ? 0.0f : f16_to_f32(r.b[k]);
+            }
+        }
+        return d;
+    }
+    // bias: lane j == 0 adds b * sum(x) over the 32 columns of each step
+    TQ_DEV static float bias(const Dec& d, const float* s16) {
+        float t = 0.0f;
+        if constexpr (!IS_FP4) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) t = __builtin_fmaf(d.b[i], s16[2 * i] + s16[2 * i + 1], t);
+        }
+        return t;
+    }
+    TQ_DEV static float fold_f32(const Raw& r, const Dec& d, int j, const float* xc, const float* s16) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float x[8];
+            ld_f8(xc + 32 * i + 8 * j, x);
+            if constexpr (IS_FP4) {
+                float a = 0.0f, b = 0.0f;
+#pragma unroll
+                for (int n = 0; n < 8; n += 2) {
+                    a = __builtin_fmaf(fp4_to_f32((r.w[i] >> (4 * n)) & 0xF), x[n], a);
+                    b = __builtin_fmaf(fp4_to_f32((r.w[i] >> (4 * n + 4)) & 0xF), x[n + 1], b);
+                }
+                t = __builtin_fmaf(d.s[i], a + b, t);
+            } else {
+                t = __builtin_fmaf(d.s[i], dot_nib8(r.w[i], x), t);
+            }
+        }
+        return j == 0 ? t + bias(d, s16) : t;
+    }
+    TQ_DEV static float fold_h(const Raw& r, const Dec& d, int j, const _Float16* xc, const float* s16) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 xv = *(const uint4*)(xc + 32 * i + 8 * j);
+            const uint32_t w = r.w[i];
+            if constexpr (IS_FP4) {
+                float a = dot2(fp4_pair(w, 0), xv.x, 0.0f);
+                float b = dot2(fp4_pair(w, 2), xv.y, 0.0f);
+                a = dot2(fp4_pair(w, 1), xv.z, a);
+                b = dot2(fp4_pair(w, 3), xv.w, b);
+                t = __builtin_fmaf(d.s[i], (a + b) * kTwo14, t);
+            } else {
+                const uint32_t u = w >> 8;
+                float lo = dot2(w & 0x000F000Fu, xv.x, 0.0f);  // (n0, n4)
+                lo = dot2(u & 0x000F000Fu, xv.y, lo);          // (n2, n6)
+                float hi = dot2(w & 0x00F000F0u, xv.z, 0.0f);  // (n1, n5) x16
+                hi = dot2(u & 0x00F000F0u, xv.w, hi);          // (n3, n7) x16
+                t = __builtin_fmaf(d.s[i], __builtin_fmaf(hi, 0.0625f, lo) * kTwo24, t);
+            }
+        }
+        return j == 0 ? t + bias(d, s16) : t;
+    }
+    // MFMA: per step one 16x16x32 for sum(q*x) and one against ones for
+    // sum(x); folded into acc at the end of each group.
+    template <int NB, int NV, int GS>
+    TQ_DEV static void fold_mfma(const Raw& r, const Dec& d, int j, const _Float16* const* xt,
+                                 f4_t* acc) {
+#ifdef TQ_EXP_NOFOLD
+        acc[0][0] += __builtin_bit_cast(float, (r.w[0] ^ r.w[1] ^ r.w[2] ^ r.w[3]) & 0x3FFFFFFF) +
+                     d.s[3] + (float)xt[0][8 * j];
+        return;
+#endif
+        const h8_t ones = h8_of(make_uint4(kOnes2, kOnes2, kOnes2, kOnes2));
+        f4_t C[NB], H[NB], O[NB];
+#pragma unroll
+        for (int n = 0; n < NB; n++) { C[n] = f4_zero(); H[n] = f4_zero(); O[n] = f4_zero(); }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t w = r.w[i], u = w >> 8;
+            const h4_t blo = h4_of(w & 0x000F000Fu, u & 0x000F000Fu);  // (n0, n4, n2, n6)
+            const h4_t bhi = h4_of(w & 0x00F000F0u, u & 0x00F000F0u);  // (n1, n5, n3, n7) x16
+#pragma unroll
+            for (int n = 0; n < NB; n++) {
+                const uint4 xv = *(const uint4*)(xt[n] + 32 * i + 8 * j);
+                C[n] = mfma16(h4_of(xv.x, xv.y), blo, C[n]);
+                H[n] = mfma16(h4_of(xv.z, xv.w), bhi, H[n]);
+                O[n] = mfma32(h8_of(xv), ones, O[n]);
+            }
+            if ((i + 1) % GS == 0) {  // end of a group
+                const float s = d.s[i] * kTwo24, sh = d.s[i] * (kTwo24 / 16.0f), bb = d.b[i];
+#pragma unroll
+                for (int n = 0; n < NB; n++) {
+#pragma unroll
+                    for (int v = 0; v < NV; v++) {
+                        float t = __builtin_fmaf(s, C[n][v], acc[n][v]);
+                        t = __builtin_fmaf(sh, H[n][v], t);
+                        acc[n][v] = __builtin_fmaf(bb, O[n][v], t);
+                    }
+                    C[n] = f4_zero();
+                    H[n] = f4_zero();
+                    O[n] = f4_zero();
+                }
+            }
+        }
+    }
+    // 8 staged activations starting at chunk column d0 (d0 % 8 == 0)
+    TQ_DEV static uint4 stage8(const _Float16* xr, int d0) {
+        _Float16 h[8], o[8];
+        ldh8(xr + d0, h);
+        o[0] = h[0]; o[1] = h[4]; o[2] = h[2]; o[3] = h[6];
+        o[4] = h[1]; o[5] = h[5]; o[6] = h[3]; o[7] = h[7];
+        return pack8(o);
+    }
+    TQ_DEV static int steps_per_group(const WDesc& w) { return w.g.gs >= 128 ? 4 : w.g.gs / 32; }
+};
+template <int L> using FxInt4 = FxNib<L, false>;
+template <int L> using FxFp4 = FxNib<L, true>;
+
+// ============================================================================
+// INT2 affine (dequant.cu:110-172): word (4i+j) = columns 64i + 16j + n of
+// the chunk (code n in bits 2n); groups >= 64 columns.  LDS order per 16
+// columns: [0,8,4,12, 1,9,5,13, 2,10,6,14, 3,11,7,15] -- the field at bits
+// 2k of the two 16-bit halves of (w, w >> 8) are codes (k, k+8) / (k+4, k+12).
+// ============================================================================
+template <int LAYOUT>
+struct FxInt2 {
+    static constexpr int FMT = TITAN_INT2, CHUNK_COLS = 256;
+    static constexpr bool HAS_MFMA = true;
+    struct Off { uint32_t c, s, b; };
+    struct Raw { uint32_t w[4], s[4], b[4]; };
+    struct Dec { float s[4], b[4]; };
+    TQ_DEV static Off base(const WDesc& w, int row, int j) {
+        const Geo& g = w.g;
+        if constexpr (LAYOUT == TITAN_LAYOUT_REF)
+            return {(uint32_t)row * (uint32_t)g.row_code_bytes + 4u * j,
+                    (uint32_t)row * (uint32_t)(g.ngroups * 2), (uint32_t)row * (uint32_t)(g.ngroups * 2)};
+        else
+            return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_sb_off(g, row, 0), 0u};
+    }
+    template <int GS>
+    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
+        if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
+        } else {
+            uint4 q = ld_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
+        }
+#pragma unroll
+        for (int i = GS - 1; i < 4; i += GS) {  // last word step of each group
+            const uint32_t grp = (uint32_t)group_of(w, c * 256 + 64 * i);
+            if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
+                r.s[i] = ld_u16(w.scales + (o.s + grp * 2u));
+                r.b[i] = ld_u16(w.biases + (o.b + grp * 2u));
+            } else {
+                r.s[i] = ld_u32(w.codes + (o.s + grp * 64u));
+            }
+        }
+    }
+    template <int GS>
+    TQ_DEV static Dec decode(const WDesc&, const Raw& r, int, int) {
+        Dec d;  // step i takes the scales loaded for the last step of its group
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int k = i | (GS - 1);
+            if constexpr (LAYOUT == TITAN_LAYOUT_TILED) {
+                d.s[i] = f16_to_f32(r.s[k] & 0xFFFF);
+                d.b[i] = f16_to_f32(r.s[k] >> 16);
+            } else {
+                d.s[i] = f16_to_f32(r.s[k]);
+                d.b[i] = f16_to_f32(r.b[k]);
+            }
+        }
+        return d;
+    }
+    TQ_DEV static float bias(const Dec& d, const float* s16) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            t = __builtin_fmaf(d.b[i], (s16[4 * i] + s16[4 * i + 1]) + (s16[4 * i + 2] + s16[4 * i + 3]), t);
+        return t;
+    }
+    TQ_DEV static float fold_f32(const Raw& r, const Dec& d, int j, const float* xc, const float* s16) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float x[16];
+            ld_f8(xc + 64 * i + 16 * j, x);
+            ld_f8(xc + 64 * i + 16 * j + 8, x + 8);
+            float a = 0.0f, b = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const uint32_t v = (r.w[i] >> (2 * s)) & 0x03030303u;  // codes s, s+4, s+8, s+12
+                a = __builtin_fmaf((float)(v & 0xFF), x[s], a);
+                b = __builtin_fmaf((float)((v >> 8) & 0xFF), x[s + 4], b);
+                a = __builtin_fmaf((float)((v >> 16) & 0xFF), x[s + 8], a);
+                b = __builtin_fmaf((float)(v >> 24), x[s + 12], b);
+            }
+            t = __builtin_fmaf(d.s[i], a + b, t);
+        }
+        return j == 0 ? t + bias(d, s16) : t;
+    }
+    TQ_DEV static float fold_h(const Raw& r, const Dec& d, int j, const _Float16* xc, const float* s16) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 xa = *(const uint4*)(xc + 64 * i + 16 * j);
+            const uint4 xb = *(const uint4*)(xc + 64 * i + 16 * j + 8);
+            const uint32_t w = r.w[i], u = w >> 8;
+            float s1 = dot2(w & 0x00030003u, xa.x, 0.0f);   // (0, 8)
+            s1 = dot2(u & 0x00030003u, xa.y, s1);           // (4, 12)
+            float s4 = dot2(w & 0x000C000Cu, xa.z, 0.0f);   // (1, 9) x4
+            s4 = dot2(u & 0x000C000Cu, xa.w, s4);           // (5, 13) x4
+            float s16v = dot2(w & 0x00300030u, xb.x, 0.0f); // (2, 10) x16
+            s16v = dot2(u & 0x00300030u, xb.y, s16v);       // (6, 14) x16
+            float s64 = dot2(w & 0x00C000C0u, xb.z, 0.0f);  // (3, 11) x64
+            s64 = dot2(u & 0x00C000C0u, xb.w, s64);         // (7, 15) x64
+            const float v = (__builtin_fmaf(s4, 0.25f, s1) + __builtin_fmaf(s64, 0.25f, s16v) * 0.0625f) * kTwo24;
+            t = __builtin_fmaf(d.s[i], v, t);
+        }
+        return j == 0 ? t + bias(d, s16) : t;
+    }
+    template <int NB, int NV, int GS>
+    TQ_DEV static void fold_mfma(const Raw& r, const Dec& d, int j, const _Float16* const* xt,
+                                 f4_t* acc) {
+        const h8_t ones = h8_of(make_uint4(kOnes2, kOnes2, kOnes2, kOnes2));
+        f4_t C[NB], O[NB];
+#pragma unroll
+        for (int n = 0; n < NB; n++) { C[n] = f4_zero(); O[n] = f4_zero(); }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t w = r.w[i];
+            // fields k = 0..3 of w and w >> 8, each shifted down to bit 0
+            const h8_t b0 = h8_of(make_uint4(w & 0x00030003u, (w >> 8) & 0x00030003u,
+                                             (w >> 2) & 0x00030003u, (w >> 10) & 0x00030003u));
+            const h8_t b1 = h8_of(make_uint4((w >> 4) & 0x00030003u, (w >> 12) & 0x00030003u,
+                                             (w >> 6) & 0x00030003u, (w >> 14) & 0x00030003u));
+#pragma unroll
+            for (int n = 0; n < NB; n++) {
+                const _Float16* p = xt[n] + 64 * i + 16 * j;
+                const uint4 xa = *(const uint4*)p;
+                const uint4 xb = *(const uint4*)(p + 8);
+                C[n] = mfma32(h8_of(xa), b0, C[n]);
+                C[n] = mfma32(h8_of(xb), b1, C[n]);
+                O[n] = mfma32(h8_of(xa), ones, O[n]);
+                O[n] = mfma32(h8_of(xb), ones, O[n]);
+            }
+            if ((i + 1) % GS == 0) {
+                const float s = d.s[i] * kTwo24, bb = d.b[i];
+#pragma unroll
+                for (int n = 0; n < NB; n++) {
+#pragma unroll
+                    for (int v = 0; v < NV; v++) {
+                        acc[n][v] = __builtin_fmaf(s, C[n][v], acc[n][v]);
+                        acc[n][v] = __builtin_fmaf(bb, O[n][v], acc[n][v]);
+                    }
+                    C[n] = f4_zero();
+                    O[n] = f4_zero();
+                }
+            }
+        }
+    }
+    TQ_DEV static uint4 stage8(const _Float16* xr, int d0) {
+        // d0 % 16 == 0: columns [0,8,4,12,1,9,5,13]; == 8: [2,10,6,14,3,11,7,15]
+        const int u = d0 & ~15, k = (d0 & 8) ? 2 : 0;
+        _Float16 a[8], b[8], o[8];
+        ldh8(xr + u, a);
+        ldh8(xr + u + 8, b);
+        o[0] = a[k]; o[1] = b[k]; o[2] = a[k + 4]; o[3] = b[k + 4];
+        o[4] = a[k + 1]; o[5] = b[k + 1]; o[6] = a[k + 5]; o[7] = b[k + 5];
+        return pack8(o);
+    }
+    TQ_DEV static int steps_per_group(const WDesc& w) { return w.g.gs >= 256 ? 4 : w.g.gs / 64; }
+};
+
+// ============================================================================
+// NVFP4 (fp4.cu:187-238): word (4i+j) = columns 32i + 8j + n (nibble n; the
+// low nibble of a byte is the even column); e4m3 scale per 16 columns, global
+// fp32 scale applied after the row sum.  LDS order as INT4.
+// ============================================================================
+template <int LAYOUT>
+struct FxNvfp4 {
+    static constexpr int FMT = TITAN_NVFP4, CHUNK_COLS = 128;
+    static constexpr bool HAS_MFMA = false;
+    struct Off { uint32_t c, s; };
+    struct Raw { uint32_t w[4]; uint32_t s0, s1; };
+    struct Dec { float s[4]; };
+    TQ_DEV static Off base(const WDesc& w, int row, int j) {
+        const Geo& g = w.g;
+        if constexpr (LAYOUT == TITAN_LAYOUT_REF)
+            return {(uint32_t)row * (uint32_t)g.row_code_bytes + 4u * j, (uint32_t)row * (uint32_t)(g.cols / 16)};
+        else
+            return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_nvs_off(g, row, 0)};
+    }
+    template <int GS>
+    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
+        if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
+            const uint8_t* sp = w.scales + (o.s + (uint32_t)c * 8u);
+            r.s0 = ld_u32(sp);
+            r.s1 = ld_u32(sp + 4);
+        } else {
+            uint4 q = ld_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
+            const uint8_t* sp = w.codes + (o.s + (uint32_t)c * 128u);
+            r.s0 = ld_u32(sp);
+            r.s1 = ld_u32(sp + 4);
+        }
+    }
+    // word step i, lane j: scale byte 2i + (j >> 1) of the chunk's 8
+    template <int GS>
+    TQ_DEV static Dec decode(const WDesc&, const Raw& r, int, int j) {
+        Dec d;
+        const int sh = 8 * (j >> 1);
+        d.s[0] = e4m3_ref_to_f32(r.s0 >> sh);
+        d.s[1] = e4m3_ref_to_f32(r.s0 >> (16 + sh));
+        d.s[2] = e4m3_ref_to_f32(r.s1 >> sh);
+        d.s[3] = e4m3_ref_to_f32(r.s1 >> (16 + sh));
+        return d;
+    }
+    TQ_DEV static float fold_f32(const Raw& r, const Dec& d, int j, const float* xc, const float*) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float x[8];
+            ld_f8(xc + 32 * i + 8 * j, x);
+            float a = 0.0f, b = 0.0f;
+#pragma unroll
+            for (int n = 0; n < 8; n += 2) {
+                a = __builtin_fmaf(fp4_to_f32((r.w[i] >> (4 * n)) & 0xF), x[n], a);
+                b = __builtin_fmaf(fp4_to_f32((r.w[i] >> (4 * n + 4)) & 0xF), x[n + 1], b);
+            }
+            t = __builtin_fmaf(d.s[i], a + b, t);
+        }
+        return t;
+    }
+    TQ_DEV static float fold_h(const Raw& r, const Dec& d, int j, const _Float16* xc, const float*) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 xv = *(const uint4*)(xc + 32 * i + 8 * j);
+            const uint32_t w = r.w[i];
+            float a = dot2(fp4_pair(w, 0), xv.x, 0.0f);
+            float b = dot2(fp4_pair(w, 2), xv.y, 0.0f);
+            a = dot2(fp4_pair(w, 1), xv.z, a);
+            b = dot2(fp4_pair(w, 3), xv.w, b);
+            t = __builtin_fmaf(d.s[i], a + b, t);
+        }
+        return t * kTwo14;
+    }
+    template <int NB, int NV, int GS>
+    TQ_DEV static void fold_mfma(const Raw&, const Dec&, int, const _Float16* const*, f4_t*) {}
+    TQ_DEV static uint4 stage8(const _Float16* xr, int d0) { return FxNib<LAYOUT>::stage8(xr, d0); }
+    TQ_DEV static int steps_per_group(const WDesc&) { return 1; }
+};
+
+// ============================================================================
+// Q4_K (ggml): chunk c = half (c & 1) of block c >> 1; word step i covers qs
+// bytes 64(c&1) + 16i .. +15 = positions l = 16(i&1) + 4j + k of the 64-element
+// group c4 = 2(c&1) + (i>>1): low nibbles are sub-block 2*c4 (column
+// 64*c4' + l), high nibbles sub-block 2*c4 + 1 (column + 32), c4' = i >> 1
+// inside the chunk.  LDS order per 64 columns: for each l4 = l/4:
+// [A(l+0), A(l+2), A(l+1), A(l+3), B(l+0), B(l+2), B(l+1), B(l+3)] with
+// A(x) = column x, B(x) = column 32 + x.
+// ============================================================================
+template <int LAYOUT>
+struct FxQ4K {
+    static constexpr int FMT = TITAN_Q4_K, CHUNK_COLS = 128;
+    static constexpr bool HAS_MFMA = true;
+    struct Off { uint32_t c, h; };
+    struct Raw { uint32_t w[4]; uint4 hdr; };
+    struct Dec { float ds[4], dm[4]; };  // [2*c4' + (0: low / 1: high)]
+    TQ_DEV static Off base(const WDesc& w, int row, int j) {
+        const Geo& g = w.g;
+        if constexpr (LAYOUT == TITAN_LAYOUT_REF)
+            return {(uint32_t)row * (uint32_t)(g.nblk * 144) + 16u + 4u * j, (uint32_t)row * (uint32_t)(g.nblk * 144)};
+        else
+            return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_q4k_hdr_off(g, row, 0)};
+    }
+    template <int GS>
+    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
+        const uint32_t blk = (uint32_t)c >> 1;
+        if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
+            r.hdr = ld_u128(w.codes + (o.h + blk * 144u));
+            const uint32_t q = o.c + blk * 144u + ((uint32_t)c & 1u) * 64u;
+#pragma unroll
+            for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (q + 16u * i));
+        } else {
+            r.hdr = ld_u128(w.codes + (o.h + blk * 256u));
+            uint4 q = ld_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
+        }
+    }
+    template <int GS>
+    TQ_DEV static Dec decode(const WDesc&, const Raw& r, int c, int) {
+        const float d = f16_to_f32(r.hdr.x & 0xFFFF), dmin = f16_to_f32(r.hdr.x >> 16);
+        Dec o;
+        const int sb0 = 4 * (c & 1);  // first sub-block of this half block
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            uint32_t sc, m;
+            q4k_scale_min(r.hdr.y, r.hdr.z, r.hdr.w, sb0 + k, sc, m);
+            o.ds[k] = d * (float)sc;
+            o.dm[k] = dmin * (float)m;
+        }
+        return o;
+    }
+    TQ_DEV static float bias(const Dec& d, const float* s16) {
+        float t = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) t = __builtin_fmaf(-d.dm[k], s16[2 * k] + s16[2 * k + 1], t);
+        return t;
+    }
+    TQ_DEV static float fold_f32(const Raw& r, const Dec& d, int j, const float* xc, const float* s16) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int base = 64 * (i >> 1) + 16 * (i & 1) + 4 * j;
+            float xa[4], xb[4];
+            ld_f4(xc + base, xa);
+            ld_f4(xc + base + 32, xb);
+            const uint32_t lo = r.w[i] & 0x0F0F0F0Fu, hi = (r.w[i] >> 4) & 0x0F0F0F0Fu;
+            float a = (float)(lo & 0xFF) * xa[0];
+            a = __builtin_fmaf((float)((lo >> 8) & 0xFF), xa[1], a);
+            a = __builtin_fmaf((float)((lo >> 16) & 0xFF), xa[2], a);
+            a = __builtin_fmaf((float)(lo >> 24), xa[3], a);
+            float b = (float)(hi & 0xFF) * xb[0];
+            b = __builtin_fmaf((float)((hi >> 8) & 0xFF), xb[1], b);
+            b = __builtin_fmaf((float)((hi >> 16) & 0xFF), xb[2], b);
+            b = __builtin_fmaf((float)(hi >> 24), xb[3], b);
+            t = __builtin_fmaf(d.ds[2 * (i >> 1)], a, t);
+            t = __builtin_fmaf(d.ds[2 * (i >> 1) + 1], b, t);
+        }
+        return j == 0 ? t + bias(d, s16) : t;
+    }
+    TQ_DEV static float fold_h(const Raw& r, const Dec& d, int j, const _Float16* xc, const float* s16) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 xv = *(const uint4*)(xc + 64 * (i >> 1) + 8 * (4 * (i & 1) + j));
+            const uint32_t w = r.w[i], u = w >> 8;
+            float a = dot2(w & 0x000F000Fu, xv.x, 0.0f);  // low nibbles, bytes (0, 2)
+            a = dot2(u & 0x000F000Fu, xv.y, a);           // bytes (1, 3)
+            float b = dot2(w & 0x00F000F0u, xv.z, 0.0f);  // high nibbles x16
+            b = dot2(u & 0x00F000F0u, xv.w, b);
+            t = __builtin_fmaf(d.ds[2 * (i >> 1)], a * kTwo24, t);
+            t = __builtin_fmaf(d.ds[2 * (i >> 1) + 1], b * (kTwo24 / 16.0f), t);
+        }
+        return j == 0 ? t + bias(d, s16) : t;
+    }
+    template <int NB, int NV, int GS>
+    TQ_DEV static void fold_mfma(const Raw& r, const Dec& d, int j, const _Float16* const* xt,
+                                 f4_t* acc) {
+        const h4_t ones = h4_of(kOnes2, kOnes2);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {  // the two 64-element groups of the chunk
+            f4_t CA[NB], CB[NB], OA[NB], OB[NB];
+#pragma unroll
+            for (int n = 0; n < NB; n++) { CA[n] = CB[n] = OA[n] = OB[n] = f4_zero(); }
+#pragma unroll
+            for (int ii = 0; ii < 2; ii++) {
+                const int i = 2 * h + ii;
+                const uint32_t w = r.w[i], u = w >> 8;
+                const h4_t blo = h4_of(w & 0x000F000Fu, u & 0x000F000Fu);
+                const h4_t bhi = h4_of(w & 0x00F000F0u, u & 0x00F000F0u);  // x16
+#pragma unroll
+                for (int n = 0; n < NB; n++) {
+                    const uint4 xv = *(const uint4*)(xt[n] + 64 * h + 8 * (4 * ii + j));
+                    const h4_t xa = h4_of(xv.x, xv.y), xb = h4_of(xv.z, xv.w);
+                    CA[n] = mfma16(xa, blo, CA[n]);
+                    CB[n] = mfma16(xb, bhi, CB[n]);
+                    OA[n] = mfma16(xa, ones, OA[n]);
+                    OB[n] = mfma16(xb, ones, OB[n]);
+                }
+            }
+            const float sa = d.ds[2 * h] * kTwo24, sb = d.ds[2 * h + 1] * (kTwo24 / 16.0f);
+            const float ma = -d.dm[2 * h], mb = -d.dm[2 * h + 1];
+#pragma unroll
+            for (int n = 0; n < NB; n++)
+#pragma unroll
+                for (int v = 0; v < NV; v++) {
+                    float a = __builtin_fmaf(sa, CA[n][v], acc[n][v]);
+                    a = __builtin_fmaf(sb, CB[n][v], a);
+                    a = __builtin_fmaf(ma, OA[n][v], a);
+                    acc[n][v] = __builtin_fmaf(mb, OB[n][v], a);
+                }
+        }
+    }
+    TQ_DEV static uint4 stage8(const _Float16* xr, int d0) {
+        const int g64 = d0 & ~63, l = ((d0 & 63) >> 3) * 4;
+        _Float16 a[4], b[4], o[8];
+        ldh4(xr + g64 + l, a);
+        ldh4(xr + g64 + 32 + l, b);
+        o[0] = a[0]; o[1] = a[2]; o[2] = a[1]; o[3] = a[3];
+        o[4] = b[0]; o[5] = b[2]; o[6] = b[1]; o[7] = b[3];
+        return pack8(o);
+    }
+    TQ_DEV static int steps_per_group(const WDesc&) { return 2; }
+};
+
+// ============================================================================
+// Q3_K (ggml, tiled layout only): chunk c = block c; word step i covers qs
+// bytes 16i + 4j + k: half h = i >> 1, position l = 16(i&1) + 4j + k; level
+// jj (bits 2jj of the byte, hmask bit 4h + jj of hmask[l]) is column
+// 128h + 32jj + l with sub-block scale 8h + 2jj + (i&1).  LDS order per
+// 256 columns: for each (h, l4 = l/4) 16 halves [jj: l+0, l+2, l+1, l+3].
+// ============================================================================
+template <int LAYOUT>
+struct FxQ3K {
+    static constexpr int FMT = TITAN_Q3_K, CHUNK_COLS = 256;
+    static constexpr bool HAS_MFMA = false;
+    struct Off { uint32_t c, h, s, d; };
+    struct Raw { uint32_t w[4]; uint32_t hm0, hm1, s0, s1, s2, dh; };
+    struct Dec { float dsc[4][4]; };  // [i][jj]
+    TQ_DEV static Off base(const WDesc& w, int row, int j) {
+        const Geo& g = w.g;
+        return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_q3k_hmask_off(g, row, 0, j),
+                (uint32_t)tiled_q3k_sc_off(g, row, 0), (uint32_t)tiled_q3k_d_off(g, row, 0)};
+    }
+    template <int GS>
+    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
+        const uint32_t b = (uint32_t)c;
+        uint4 q = ld_u128(w.codes + (o.c + b * 1024u));
+        r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
+        const uint8_t* hp = w.codes + (o.h + b * 512u);
+        r.hm0 = ld_u32(hp);
+        r.hm1 = ld_u32(hp + 4);
+        const uint8_t* sp = w.codes + (o.s + b * 192u);
+        r.s0 = ld_u32(sp);
+        r.s1 = ld_u32(sp + 4);
+        r.s2 = ld_u32(sp + 8);
+        r.dh = ld_u16(w.codes + (o.d + b * 32u));
+    }
+    template <int GS>
+    TQ_DEV static Dec decode(const WDesc&, const Raw& r, int, int) {
+        Dec o;
+        const float d = f16_to_f32(r.dh);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+                o.dsc[i][jj] = d * (float)q3k_scale(r.s0, r.s1, r.s2, 8 * (i >> 1) + 2 * jj + (i & 1));
+        return o;
+    }
+    // 3-bit code u = q2 + 4 * hbit of the 4 bytes of word step i at level jj
+    TQ_DEV static uint32_t code3(const Raw& r, int i, int jj) {
+        const uint32_t hm = (i & 1) ? r.hm1 : r.hm0;
+        return ((r.w[i] >> (2 * jj)) & 0x03030303u) | (((hm >> (4 * (i >> 1) + jj)) & 0x01010101u) << 2);
+    }
+    TQ_DEV static float bias(const Dec& d, const float* s16) {
+        // value = d*sc*(u - 4): the -4 term is -4 d sc sum(x) per sub-block
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+                t = __builtin_fmaf(-4.0f * d.dsc[i][jj], s16[8 * (i >> 1) + 2 * jj + (i & 1)], t);
+        return t;
+    }
+    TQ_DEV static float fold_f32(const Raw& r, const Dec& d, int j, const float* xc, const float* s16) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                float x[4];
+                ld_f4(xc + 128 * (i >> 1) + 32 * jj + 16 * (i & 1) + 4 * j, x);
+                const uint32_t v = code3(r, i, jj);
+                float a = (float)(v & 0xFF) * x[0];
+                a = __builtin_fmaf((float)((v >> 8) & 0xFF), x[1], a);
+                a = __builtin_fmaf((float)((v >> 16) & 0xFF), x[2], a);
+                a = __builtin_fmaf((float)(v >> 24), x[3], a);
+                t = __builtin_fmaf(d.dsc[i][jj], a, t);
+            }
+        return j == 0 ? t + bias(d, s16) : t;
+    }
+    TQ_DEV static float fold_h(const Raw& r, const Dec& d, int j, const _Float16* xc, const float* s16) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const _Float16* p = xc + 16 * (8 * (i >> 1) + 4 * (i & 1) + j);
+            const uint4 x01 = *(const uint4*)p, x23 = *(const uint4*)(p + 8);
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const uint32_t v = code3(r, i, jj);
+                const uint32_t xa = jj == 0 ? x01.x : jj == 1 ? x01.z : jj == 2 ? x23.x : x23.z;
+                const uint32_t xb = jj == 0 ? x01.y : jj == 1 ? x01.w : jj == 2 ? x23.y : x23.w;
+                float a = dot2(v & 0x00070007u, xa, 0.0f);
+                a = dot2((v >> 8) & 0x00070007u, xb, a);
+                t = __builtin_fmaf(d.dsc[i][jj], a, t);
+            }
+        }
+        t *= kTwo24;
+        return j == 0 ? t + bias(d, s16) : t;
+    }
+    template <int NB, int NV, int GS>
+    TQ_DEV static void fold_mfma(const Raw&, const Dec&, int, const _Float16* const*, f4_t*) {}
+    TQ_DEV static uint4 stage8(const _Float16* xr, int d0) {
+        // d0 = 16 * (8h + l4) + 8 * p: levels jj = 2p, 2p+1 of positions l..l+3
+        const int e = d0 >> 4, h = e >> 3, l = (e & 7) * 4, jj = (d0 & 8) ? 2 : 0;
+        _Float16 a[4], b[4], o[8];
+        ldh4(xr + 128 * h + 32 * jj + l, a);
+        ldh4(xr + 128 * h + 32 * (jj + 1) + l, b);
+        o[0] = a[0]; o[1] = a[2]; o[2] = a[1]; o[3] = a[3];
+        o[4] = b[0]; o[5] = b[2]; o[6] = b[1]; o[7] = b[3];
+        return pack8(o);
+    }
+    TQ_DEV static int steps_per_group(const WDesc&) { return 1; }
+};
+
+// ============================================================================
+// FP8 E4M3 with a per-row fp32 scale applied after the row sum: word (4i+j) =
+// columns 16i + 4j + k.  LDS order per 4 columns [0, 2, 1, 3].
+// ============================================================================
+template <int LAYOUT>
+struct FxFp8 {
+    static constexpr int FMT = TITAN_FP8_E4M3, CHUNK_COLS = 64;
+    static constexpr bool HAS_MFMA = false;
+    struct Off { uint32_t c; };
+    struct Raw { uint32_t w[4]; };
+    struct Dec {};
+    TQ_DEV static Off base(const WDesc& w, int row, int j) {
+        if constexpr (LAYOUT == TITAN_LAYOUT_REF)
+            return {(uint32_t)row * (uint32_t)w.g.row_code_bytes + 4u * j};
+        else
+            return {(uint32_t)tiled_code_off(w.g, row, 0, j)};
+    }
+    template <int GS>
+    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
+        if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
+        } else {
+            uint4 q = ld_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
+        }
+    }
+    template <int GS>
+    TQ_DEV static Dec decode(const WDesc&, const Raw&, int, int) { return {}; }
+    TQ_DEV static float fold_f32(const Raw& r, const Dec&, int j, const float* xc, const float*) {
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float x[4];
+            ld_f4(xc + 16 * i + 4 * j, x);
+            a = __builtin_fmaf(e4m3_ocp_to_f32(r.w[i]), x[0], a);
+            b = __builtin_fmaf(e4m3_ocp_to_f32(r.w[i] >> 8), x[1], b);
+            a = __builtin_fmaf(e4m3_ocp_to_f32(r.w[i] >> 16), x[2], a);
+            b = __builtin_fmaf(e4m3_ocp_to_f32(r.w[i] >> 24), x[3], b);
+        }
+        return a + b;
+    }
+    TQ_DEV static float fold_h(const Raw& r, const Dec&, int j, const _Float16* xc, const float*) {
+        // e4m3 byte -> fp16 bits by shifting: value * 2^-8, exact (the NaN
+        // codes are not produced by quantizers and are not special-cased)
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint2 xv = *(const uint2*)(xc + 16 * i + 4 * j);
+            const uint32_t w = r.w[i], u = w >> 8;
+            a = dot2(((w & 0x007F007Fu) << 7) | ((w & 0x00800080u) << 8), xv.x, a);
+            b = dot2(((u & 0x007F007Fu) << 7) | ((u & 0x00800080u) << 8), xv.y, b);
+        }
+        return (a + b) * 256.0f;
+    }
+    template <int NB, int NV, int GS>
+    TQ_DEV static void fold_mfma(const Raw&, const Dec&, int, const _Float16* const*, f4_t*) {}
+    TQ_DEV static uint4 stage8(const _Float16* xr, int d0) {
+        _Float16 h[8], o[8];
+        ldh8(xr + d0, h);
+        o[0] = h[0]; o[1] = h[2]; o[2] = h[1]; o[3] = h[3];
+        o[4] = h[4]; o[5] = h[6]; o[6] = h[5]; o[7] = h[7];
+        return pack8(o);
+    }
+    TQ_DEV static int steps_per_group(const WDesc&) { return 1; }
+};
+
+}  // namespace tq

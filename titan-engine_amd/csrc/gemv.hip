@@ -51,17 +51,22 @@ int check_weight(const titan_qweight* W) {
 
 // Can the fast kernel serve this weight?  (Tiled always can.)
 bool fast_ok(const titan_qweight* W) {
-    if (W->layout == TITAN_LAYOUT_TILED) return true;
+    if (W->layout == TITAN_LAYOUT_TILED)  // tiled_total_bytes admits only fast shapes
+        return ((uintptr_t)W->codes & 15) == 0;
     const int f = W->format, cols = W->cols, gs = W->group_size;
-    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-    if (!al16(W->codes)) return false;
-    switch (f) {
-        case TITAN_INT4: case TITAN_FP4: return cols % 32 == 0 && gs % 32 == 0;
-        case TITAN_INT2: return cols % 64 == 0 && gs % 64 == 0;
-        case TITAN_NVFP4: return cols % 32 == 0 && ((uintptr_t)W->scales & 1) == 0;
+    auto al4 = [](const void* p) { return ((uintptr_t)p & 3) == 0; };
+    if (!al4(W->codes)) return false;
+    // 32-bit per-lane offsets
+    if ((uint64_t)W->rows * (uint64_t)W->cols >= (1ull << 32)) return false;
+    const bool pow2 = gs > 0 && (gs & (gs - 1)) == 0;
+    switch (f) {  // whole 64-byte chunks per row; groups cover whole word steps
+        case TITAN_INT4: case TITAN_FP4:
+            return cols % 128 == 0 && gs % 32 == 0 && pow2 && ((uintptr_t)W->scales & 1) == 0;
+        case TITAN_INT2: return cols % 256 == 0 && gs % 64 == 0 && pow2;
+        case TITAN_NVFP4: return cols % 128 == 0 && al4(W->scales);
         case TITAN_Q4_K: return true;
         case TITAN_Q3_K: return false;  // 110-byte blocks: generic path
-        case TITAN_FP8_E4M3: return cols % 16 == 0;
+        case TITAN_FP8_E4M3: return cols % 64 == 0;
     }
     return false;
 }
@@ -73,7 +78,7 @@ WDesc make_wdesc(const titan_qweight* W) {
     d.biases = (const uint8_t*)W->biases;
     d.g = make_geo(W->format, W->rows, W->cols, W->group_size);
     d.gscale = W->global_scale;
-    d.gshift = -1;
+    d.gshift = 0;  // fast-path groups are powers of two
     for (int sh = 0; sh < 31; sh++)
         if (W->group_size == (1 << sh)) d.gshift = sh;
     return d;
@@ -102,6 +107,7 @@ int run_gemv(const titan_qweight* Ws, const void* const* Xs, const int64_t* ldx,
     a.xdt = xdt;
     a.ydt = ydt;
     int total_tiles = 0;
+    bool f16 = xdt == TITAN_FP16;
     for (int i = 0; i < n; i++) {
         GemvProb& p = a.p[i];
         p.w = make_wdesc(&Ws[i]);
@@ -109,9 +115,14 @@ int run_gemv(const titan_qweight* Ws, const void* const* Xs, const int64_t* ldx,
         p.y = Ys[i];
         p.ldx = ldx[i];
         p.ldy = ldy[i];
-        p.nchunks = (Ws[i].cols + chunk_cols_of(fmt) - 1) / chunk_cols_of(fmt);
+        p.nchunks = Ws[i].cols / chunk_cols_of(fmt);
         p.ntiles = (Ws[i].rows + 15) / 16;
+        // MFMA word steps per scale group (INT4: 32 columns a step, INT2: 64)
+        const int spc = fmt == TITAN_INT2 ? 64 : 32;
+        const int gs = Ws[i].group_size;
+        p.gsteps = gs >= 4 * spc ? 4 : (gs >= spc ? gs / spc : 1);
         total_tiles += p.ntiles;
+        f16 = f16 && ((uintptr_t)Xs[i] & 15) == 0 && (ldx[i] & 7) == 0;
     }
     if (!fast) {
         // the generic kernel serves one problem per launch
@@ -135,17 +146,36 @@ int run_gemv(const titan_qweight* Ws, const void* const* Xs, const int64_t* ldx,
         }
         return tqh::launch_status();
     }
-    for (int m0 = 0; m0 < M; m0 += 8) {
+    bool has_mfma = false;
+    switch (fmt) {
+        case TITAN_INT4: has_mfma = gemv_has_mfma_int4(); break;
+        case TITAN_INT2: has_mfma = gemv_has_mfma_int2(); break;
+        case TITAN_Q4_K: has_mfma = gemv_has_mfma_q4k(); break;
+        default: break;
+    }
+    // one group size per launch (the kernels take the word steps per group
+    // as a template parameter); mixed group sizes go one problem at a time
+    for (int i = 1; i < n; i++)
+        if (a.p[i].gsteps != a.p[0].gsteps) {
+            for (int q = 0; q < n; q++) {
+                int s = run_gemv(&Ws[q], &Xs[q], &ldx[q], &Ys[q], &ldy[q], 1, xdt, ydt, M, st);
+                if (s) return s;
+            }
+            return TITAN_OK;
+        }
+    const int mode = !f16 ? kModeF32 : (has_mfma ? kModeMfma : kModeDot2);
+    const int per_launch = mode == kModeMfma ? 32 : 8;
+    for (int m0 = 0; m0 < M; m0 += per_launch) {
         a.m0 = m0;
-        int mc = M - m0 < 8 ? M - m0 : 8;
+        int mc = M - m0 < per_launch ? M - m0 : per_launch;
         switch (fmt) {
-            case TITAN_INT4: dispatch_gemv_int4(a, layout, mc, total_tiles, st); break;
-            case TITAN_INT2: dispatch_gemv_int2(a, layout, mc, total_tiles, st); break;
-            case TITAN_FP4: dispatch_gemv_fp4(a, layout, mc, total_tiles, st); break;
-            case TITAN_NVFP4: dispatch_gemv_nvfp4(a, layout, mc, total_tiles, st); break;
-            case TITAN_Q4_K: dispatch_gemv_q4k(a, layout, mc, total_tiles, st); break;
-            case TITAN_Q3_K: dispatch_gemv_q3k(a, layout, mc, total_tiles, st); break;
-            default: dispatch_gemv_fp8(a, layout, mc, total_tiles, st); break;
+            case TITAN_INT4: dispatch_gemv_int4(a, layout, mc, mode, total_tiles, st); break;
+            case TITAN_INT2: dispatch_gemv_int2(a, layout, mc, mode, total_tiles, st); break;
+            case TITAN_FP4: dispatch_gemv_fp4(a, layout, mc, mode, total_tiles, st); break;
+            case TITAN_NVFP4: dispatch_gemv_nvfp4(a, layout, mc, mode, total_tiles, st); break;
+            case TITAN_Q4_K: dispatch_gemv_q4k(a, layout, mc, mode, total_tiles, st); break;
+            case TITAN_Q3_K: dispatch_gemv_q3k(a, layout, mc, mode, total_tiles, st); break;
+            default: dispatch_gemv_fp8(a, layout, mc, mode, total_tiles, st); break;
         }
     }
     return tqh::launch_status();

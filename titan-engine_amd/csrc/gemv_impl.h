@@ -1,122 +1,111 @@
-// gemv.hip -- dequant-GEMV / small-M dequant-GEMM for decode (VALU path).
+// gemv_impl.h -- dequant-GEMV / small-M dequant-GEMM kernels for decode.
 //
 // Replaces the reference's one-block-per-row kernels (dequant.cu:23-172,
 // fp4.cu:28-84, fp4.cu:187-238).  Design for gfx950:
 //  * A workgroup of 4 waves owns RT tiles of 16 rows and the whole K range.
-//    The waves split K (wave w takes 64-byte chunks w, w+4, ...), so at any
-//    moment the workgroup streams 256 contiguous code bytes per row, and each
-//    wave keeps its next chunk's loads in flight while folding the current.
-//  * Lane l = 16*j + r loads row r's 16-byte slot j of a chunk with one
-//    128-bit load; in the tiled layout a wave's 64 loads are 1 KiB contiguous.
-//  * Activations are staged once per workgroup into LDS as fp32 (phases of
-//    at most 40 KiB for long K / many tokens) and read back as 128-bit
-//    vectors; each activation segment is reused across the RT row tiles.
-//  * Dequantization happens in registers: affine formats fold as
-//    scale * sum(q*x) + bias * sum(x); lanes of a row are reduced with two
-//    cross-lane shuffles, waves through LDS.
+//    The waves split K (wave w takes 64-byte chunks w, w+4, ...): the
+//    workgroup streams 256 contiguous code bytes per row at a time.
+//  * Each wave holds two groups of U chunks of codes in registers, so the
+//    next group's loads (4 KiB per wave) are in flight while the current one
+//    is folded; loads never depend on a branch.
+//  * Activations are staged per workgroup into LDS (phases of at most
+//    kGemvLdsBytes for long K / many tokens): fp32 in column order for fp32 /
+//    bf16 inputs, fp16 in each format's pairing order for fp16 inputs.
+//  * Folding (fast.h): fp32 FMA, packed fp16 dot products, or MFMA with the
+//    activations as the A operand and the codes as exact fp16 subnormals.
+//  * Lanes of a row (VALU modes) are reduced with two cross-lane shuffles,
+//    waves through LDS; MFMA accumulators already hold whole-row sums.
 #pragma once
-#include "formats.h"
+#include "fast.h"
 
 namespace tq {
 
 constexpr int kGemvWaves = 4;
 constexpr int kGemvThreads = kGemvWaves * kWave;
-constexpr int kGemvLdsBytes = 16 * 1024;  // activation stage per workgroup
+constexpr int kGemvLdsBytes = 32 * 1024;  // activation stage per workgroup
+
+enum { kModeF32 = 0, kModeDot2 = 1, kModeMfma = 2 };
 
 struct GemvProb {
     WDesc w;
     const void* x;
     void* y;
     int64_t ldx, ldy;
-    int nchunks;   // ceil(cols / CHUNK_COLS)
+    int nchunks;   // cols / CHUNK_COLS
     int wg_begin;  // first workgroup of this problem
     int ntiles;    // ceil(rows / 16)
+    int gsteps;    // MFMA word steps per scale group (power of two <= 4)
+    int ks_log;    // log2 of the waves sharing one row tile (K split)
 };
 
 struct GemvArgs {
     GemvProb p[TITAN_MAX_BATCH];
     int n;
     int xdt, ydt;
-    int m0;   // first token of this launch (launches cover <= 8 tokens)
+    int m0;      // first token of this launch
     int mcount;  // tokens in this launch (<= the kernel's template width)
-    int pc;   // staged columns per phase (multiple of kGemvWaves * CHUNK_COLS)
+    int pc;      // staged columns per phase (whole groups of chunks)
 };
 
-// Stage x[m0 .. m0+M)[col0 .. col0+ncols) into lds[m][0 .. ncols) as fp32.
+// fp32 activations in column order plus fp32 sums of every 16 columns.
 template <int M>
-TQ_DEV void stage_x(float* lds, int pc, const void* x, int xdt, int64_t ldx, int m0, int mcount,
-                    int col0, int ncols, int tid) {
+TQ_DEV void stage_f32(float* xf, float* s16, int pc, const void* x, int xdt, int64_t ldx,
+                      int m0, int mcount, int col0, int ncols, int tid) {
 #pragma unroll
     for (int m = 0; m < M; m++) {
         const int64_t off = (int64_t)(m0 + m) * ldx + col0;
-        float* dst = lds + m * pc;
-        if (m >= mcount) {  // padding token of a narrower launch
-            for (int c = tid; c < ncols; c += kGemvThreads) dst[c] = 0.0f;
-        } else if (xdt == TITAN_FP32) {
-            const float* src = (const float*)x + off;
-            for (int c = tid; c < ncols; c += kGemvThreads) dst[c] = src[c];
-        } else if (xdt == TITAN_FP16) {
-            const _Float16* src = (const _Float16*)x + off;
-            for (int c = tid; c < ncols; c += kGemvThreads) dst[c] = (float)src[c];
-        } else {
-            const uint16_t* src = (const uint16_t*)x + off;
-            for (int c = tid; c < ncols; c += kGemvThreads) dst[c] = bf16_to_f32(src[c]);
+        float* dst = xf + m * pc;
+        for (int c = tid; c < ncols; c += kGemvThreads)
+            dst[c] = m < mcount ? load_act(x, off + c, xdt) : 0.0f;
+    }
+    __syncthreads();
+    for (int e = tid; e < M * (ncols >> 4); e += kGemvThreads) {
+        const int m = e / (ncols >> 4), g = e % (ncols >> 4);
+        const float* p = xf + m * pc + 16 * g;
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            a += p[i];
+            b += p[i + 1];
         }
+        s16[m * (pc >> 4) + g] = a + b;
     }
 }
 
-// fp16 activations: stage x[m0 .. m0+M)[col0 .. col0+ncols) as fp16,
-// permuted inside groups of PERM columns so that one 128-bit LDS read gives
-// the activation pairs a format's masked code pairs multiply (PERM 8:
-// (n, n+4); 16: (n, n+8); 4: (0, 2), (1, 3)), plus the fp32 sum of every 16
-// columns.  ncols is a multiple of 16 and rows of x are 16-byte aligned.
-template <int M, int PERM>
-TQ_DEV void stage_x_h(_Float16* xh, float* xs, int pc, const void* x, int64_t ldx, int m0,
+// fp16 activations in the format's pairing order (F::stage8) and, for the
+// VALU fold, fp32 sums of every 16 columns.  Rows of x are 16-byte aligned.
+template <class F, int M, bool SUMS>
+TQ_DEV void stage_f16(_Float16* xh, float* s16, int pc, const void* x, int64_t ldx, int m0,
                       int mcount, int col0, int ncols, int tid) {
 #pragma unroll
     for (int m = 0; m < M; m++) {
         const _Float16* src = (const _Float16*)x + (int64_t)(m0 + m) * ldx + col0;
-        for (int c = tid * 16; c < ncols; c += kGemvThreads * 16) {
-            _Float16 h[16], o[16];
+        for (int d0 = tid * 8; d0 < ncols; d0 += kGemvThreads * 8)
+            *(uint4*)(xh + m * pc + d0) = m < mcount ? F::stage8(src, d0) : make_uint4(0, 0, 0, 0);
+    }
+    if constexpr (SUMS) {
+        for (int e = tid; e < M * (ncols >> 4); e += kGemvThreads) {
+            const int m = e / (ncols >> 4), g = e % (ncols >> 4);
+            float s = 0.0f;
             if (m < mcount) {
-                const uint4 a = *(const uint4*)(src + c), b = *(const uint4*)(src + c + 8);
-                const uint32_t v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                const _Float16* src = (const _Float16*)x + (int64_t)(m0 + m) * ldx + col0 + 16 * g;
+                _Float16 h[8], k[8];
+                ldh8(src, h);
+                ldh8(src + 8, k);
+                float a = 0.0f, b = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
-                    h[2 * i] = __builtin_bit_cast(_Float16, (uint16_t)(v[i] & 0xFFFF));
-                    h[2 * i + 1] = __builtin_bit_cast(_Float16, (uint16_t)(v[i] >> 16));
+                    a += (float)h[i];
+                    b += (float)k[i];
                 }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 16; i++) h[i] = (_Float16)0.0f;
+                s = a + b;
             }
-            float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; i += 2) {
-                s0 += (float)h[i];
-                s1 += (float)h[i + 1];
-            }
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                int g, n, src_i;
-                if constexpr (PERM == 8) { g = i & 8; n = (i & 7) >> 1; src_i = g + n + 4 * (i & 1); }
-                else if constexpr (PERM == 16) { n = i >> 1; src_i = n + 8 * (i & 1); }
-                else { g = i & 12; n = i & 3; src_i = g + (n == 1 ? 2 : n == 2 ? 1 : n); }
-                o[i] = h[src_i];
-            }
-            uint32_t ov[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++)
-                ov[i] = (uint32_t)__builtin_bit_cast(uint16_t, o[2 * i]) |
-                        ((uint32_t)__builtin_bit_cast(uint16_t, o[2 * i + 1]) << 16);
-            *(uint4*)(xh + m * pc + c) = make_uint4(ov[0], ov[1], ov[2], ov[3]);
-            *(uint4*)(xh + m * pc + c + 8) = make_uint4(ov[4], ov[5], ov[6], ov[7]);
-            xs[m * (pc / 16) + c / 16] = s0 + s1;
+            s16[m * (pc >> 4) + g] = s;
         }
     }
 }
 
-template <class F, int M, int RT, bool HX>
+template <class F, int M, int MODE, int GS = 4>
 __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     int bid = blockIdx.x, pi = 0;
@@ -124,159 +113,161 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
         if (bid >= a.p[i].wg_begin) pi = i;
     const GemvProb& P = a.p[pi];
     const WDesc& W = P.w;
-    const int rows = W.g.rows, cols = W.g.cols, nchunks = P.nchunks;
+    const int rows = W.g.rows, nchunks = P.nchunks;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int r = lane & 15, j = lane >> 4;
-    const int tile0 = (bid - P.wg_begin) * RT;
+    // KS waves share one row tile and split its chunks (part, part + KS, ...)
+    const int ks_log = P.ks_log, KS = 1 << ks_log;
+    const int part = wave & (KS - 1);
+    const int tile = (bid - P.wg_begin) * (kGemvWaves >> ks_log) + (wave >> ks_log);
     const int pc = a.pc;
 
-    int rowt[RT];
-#pragma unroll
-    for (int t = 0; t < RT; t++) {
-        int row = (tile0 + t) * 16 + r;
-        rowt[t] = row < rows ? row : rows - 1;  // clamp loads; stores are masked
-    }
+    float* xf = lds;
+    _Float16* xh = (_Float16*)lds;
+    float* s16 = MODE == kModeF32 ? lds + M * pc : lds + M * pc / 2;
 
-    float acc[RT][M];
-#pragma unroll
-    for (int t = 0; t < RT; t++)
-#pragma unroll
-        for (int m = 0; m < M; m++) acc[t][m] = 0.0f;
+    const int row = tile * 16 + r;
+    const typename F::Off off = F::base(W, row < rows ? row : rows - 1, j);  // past the end: not stored
 
-    // Wave w folds chunks w, w + 4, w + 8, ... in groups of U; two groups of
-    // codes are held in registers so that the next group's loads (U*RT KiB
-    // per wave) are in flight while the current group is folded.  Every wave
-    // runs the same number of groups (out-of-range chunks are masked) so the
-    // activation-staging barriers line up.
-    constexpr int U = 4 / RT;
-    constexpr int GCH = kGemvWaves * U;  // chunks consumed per group by the workgroup
-    const int ngroups = (nchunks + GCH - 1) / GCH;
-    const int pgroups = pc / (F::CHUNK_COLS * GCH);  // groups per staged phase
+    constexpr int NB = (M + 15) / 16;  // MFMA token blocks
+    constexpr int NV = M < 4 ? M : 4;  // accumulator entries holding tokens
+    f4_t macc[NB];
+    float acc[M];
+#pragma unroll
+    for (int n = 0; n < NB; n++) macc[n] = f4_zero();
+#pragma unroll
+    for (int m = 0; m < M; m++) acc[m] = 0.0f;
 
-    auto chunk_of = [&](int g, int u) { return (g * U + u) * kGemvWaves + wave; };
-    auto valid = [&](int cc) { return cc < nchunks && cc * F::CHUNK_COLS + j * F::SLOT_COLS < cols; };
-    // Loads are unconditional (a masked chunk re-reads chunk 0, slot 0, which
-    // always exists), so no branch forces an early wait on loads in flight.
-    auto load_group = [&](int g, typename F::Raw (&R)[U][RT]) {
+    // The wave's chunks come in groups of U; the next group's loads are in
+    // flight while the current group is folded.  Every wave runs the same
+    // number of groups (chunks past the end are masked) so the staging
+    // barriers line up.
+    constexpr int U = 4;
+    // chunks per phase: the LDS stage (pc columns) or the whole row, in
+    // whole rounds of U chunks for each of the KS waves
+    const int round = U << ks_log;
+    const int pchunks = min(pc / F::CHUNK_COLS, (nchunks + round - 1) / round * round);
+    const int gpp = pchunks / round;                // groups per phase per wave
+    const int nph = (nchunks + pchunks - 1) / pchunks;
+    const int ngroups = nph * gpp;
+
+    // group q: phase q / gpp, chunks phase0 + ((q % gpp) * U + u) * KS + part
+    auto chunk_of = [&](int q, int u) {
+        const int ph = q / gpp;
+        return ph * pchunks + (((q - ph * gpp) * U + u) << ks_log) + part;
+    };
+    auto load_group = [&](int q, typename F::Raw (&R)[U]) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int cc = chunk_of(g, u);
-            const bool ok = valid(cc);
-#pragma unroll
-            for (int t = 0; t < RT; t++) F::load(W, rowt[t], ok ? cc : 0, ok ? j : 0, R[u][t]);
+            const int cc = chunk_of(q, u);
+            F::template load<GS>(W, off, cc < nchunks ? cc : 0, j, R[u]);
         }
     };
-    auto fold_group = [&](int g, const typename F::Raw (&R)[U][RT]) {
-        if (g % pgroups == 0) {  // first group of a phase: stage its activations
-            const int col0 = (g / pgroups) * pc;
+    auto fold_group = [&](int q, const typename F::Raw (&R)[U]) {
+        const int ph = q / gpp;
+        if (q == ph * gpp) {  // first group of a phase: stage its activations
+            const int col0 = ph * pchunks * F::CHUNK_COLS;
+            const int ncols = min(pchunks * F::CHUNK_COLS, W.g.cols - col0);
             __syncthreads();
-            if constexpr (HX)
-                stage_x_h<M, F::PERM>((_Float16*)lds, lds + M * pc / 2, pc, P.x, P.ldx, a.m0,
-                                      a.mcount, col0, min(pc, cols - col0), tid);
+            if constexpr (MODE == kModeF32)
+                stage_f32<M>(xf, s16, pc, P.x, a.xdt, P.ldx, a.m0, a.mcount, col0, ncols, tid);
             else
-                stage_x<M>(lds, pc, P.x, a.xdt, P.ldx, a.m0, a.mcount, col0,
-                           min(pc, cols - col0), tid);
+                stage_f16<F, M, MODE == kModeDot2>(xh, s16, pc, P.x, P.ldx, a.m0, a.mcount, col0, ncols, tid);
             __syncthreads();
         }
-        const int col0 = (g / pgroups) * pc;
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int cc = chunk_of(g, u);
-            if (!valid(cc)) continue;
-            const int lbase = cc * F::CHUNK_COLS - col0;
-            typename F::Dec dec[RT];
+            const int cc = chunk_of(q, u);
+            if (cc >= nchunks) continue;  // uniform per wave
+            const int lbase = (cc - ph * pchunks) * F::CHUNK_COLS;
+            const typename F::Dec dec = F::template decode<GS>(W, R[u], cc, j);
+            if constexpr (MODE == kModeMfma) {
+                // A-operand rows of padding tokens re-read token 0: they only
+                // feed accumulator rows that are never stored
+                const _Float16* xt[NB];
 #pragma unroll
-            for (int t = 0; t < RT; t++) dec[t] = F::decode(W, R[u][t], cc, j);
-            if constexpr (HX) {
-                const _Float16* xh = (const _Float16*)lds;
-                const float* xsum = lds + M * pc / 2;
+                for (int n = 0; n < NB; n++) {
+                    const int tok = 16 * n + r;
+                    xt[n] = xh + (tok < M ? tok : 0) * pc + lbase;
+                }
+                F::template fold_mfma<NB, NV, GS>(R[u], dec, j, xt, macc);
+            } else {
 #pragma unroll
                 for (int m = 0; m < M; m++) {
-#pragma unroll
-                    for (int s = 0; s < F::SEGS; s++) {
-                        const int lc = lbase + F::seg_col(j, s);
-                        const uint4* xp = (const uint4*)(xh + m * pc + lc);
-                        float sx = 0.0f;
-                        if constexpr (F::NEEDS_SX) {
-#pragma unroll
-                            for (int q = 0; q < F::SEGW / 16; q++) sx += xsum[m * (pc / 16) + lc / 16 + q];
-                        }
-#pragma unroll
-                        for (int t = 0; t < RT; t++) acc[t][m] += F::seg_dot_h(R[u][t], dec[t], s, xp, sx);
-                    }
-                }
-                continue;
-            }
-#pragma unroll
-            for (int m = 0; m < M; m++) {
-#pragma unroll
-                for (int s = 0; s < F::SEGS; s++) {
-                    float xv[F::SEGW];
-                    const float4* xp = (const float4*)&lds[m * pc + lbase + F::seg_col(j, s)];
-#pragma unroll
-                    for (int v = 0; v < F::SEGW / 4; v++) {
-                        float4 q = xp[v];
-                        xv[4 * v] = q.x;
-                        xv[4 * v + 1] = q.y;
-                        xv[4 * v + 2] = q.z;
-                        xv[4 * v + 3] = q.w;
-                    }
-                    float sx = 0.0f;
-                    if constexpr (F::NEEDS_SX) {
-                        float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-                        for (int v = 0; v < F::SEGW; v += 2) {
-                            s0 += xv[v];
-                            s1 += xv[v + 1];
-                        }
-                        sx = s0 + s1;
-                    }
-#pragma unroll
-                    for (int t = 0; t < RT; t++) acc[t][m] += F::seg_dot(R[u][t], dec[t], s, xv, sx);
+                    if constexpr (MODE == kModeF32)
+                        acc[m] += F::fold_f32(R[u], dec, j, xf + m * pc + lbase,
+                                              s16 + m * (pc >> 4) + (lbase >> 4));
+                    else
+                        acc[m] += F::fold_h(R[u], dec, j, xh + m * pc + lbase,
+                                            s16 + m * (pc >> 4) + (lbase >> 4));
                 }
             }
         }
     };
 
-    typename F::Raw ra[U][RT], rb[U][RT];
+    typename F::Raw ra[U], rb[U];
     load_group(0, ra);
-    for (int g = 0; g < ngroups; g += 2) {
-        if (g + 1 < ngroups) load_group(g + 1, rb);
-        fold_group(g, ra);
-        if (g + 1 >= ngroups) break;
-        if (g + 2 < ngroups) load_group(g + 2, ra);
-        fold_group(g + 1, rb);
+    for (int q = 0; q < ngroups; q += 2) {
+        if (q + 1 < ngroups) load_group(q + 1, rb);
+        fold_group(q, ra);
+        if (q + 1 >= ngroups) break;
+        if (q + 2 < ngroups) load_group(q + 2, ra);
+        fold_group(q + 1, rb);
     }
 
-    // reduce: 4 slots of a row inside the wave, then the waves via LDS
+    // per-lane results: MFMA lane (r, q = j) holds tokens 16n + 4j + v of row
+    // r; VALU lanes hold partial sums of row r over their words.
+    float res[M];
 #pragma unroll
-    for (int t = 0; t < RT; t++)
+    for (int m = 0; m < M; m++) res[m] = 0.0f;
+    if constexpr (MODE == kModeMfma) {
 #pragma unroll
-        for (int m = 0; m < M; m++) acc[t][m] = sum_slots(acc[t][m]);
-    __syncthreads();
-    if (j == 0) {
+        for (int n = 0; n < NB; n++)
 #pragma unroll
-        for (int t = 0; t < RT; t++)
+            for (int v = 0; v < 4; v++) {
+                const int tok = 16 * n + 4 * j + v;
 #pragma unroll
-            for (int m = 0; m < M; m++) lds[((wave * RT + t) * M + m) * 16 + r] = acc[t][m];
+                for (int m = 0; m < M; m++)
+                    if (m == tok) res[m] = macc[n][v];
+            }
+    } else {
+#pragma unroll
+        for (int m = 0; m < M; m++) res[m] = sum_slots(acc[m]);
     }
-    __syncthreads();
-    for (int o = tid; o < RT * M * 16; o += kGemvThreads) {
-        const int rr = o & 15, m = (o >> 4) % M, t = (o >> 4) / M;
-        const int row = (tile0 + t) * 16 + rr;
-        float v = 0.0f;
+    // waves sharing a tile (KS > 1) add up through LDS: red[wave][token][row]
+    if (KS > 1) {
+        __syncthreads();
 #pragma unroll
-        for (int w = 0; w < kGemvWaves; w++) v += lds[((w * RT + t) * M + m) * 16 + rr];
-        if (row < rows && m < a.mcount) {
-            if constexpr (F::FMT == TITAN_NVFP4) v *= W.gscale;
-            if constexpr (F::FMT == TITAN_FP8_E4M3) v *= ((const float*)W.scales)[row];
-            store_out(P.y, (int64_t)(a.m0 + m) * P.ldy + row, a.ydt, v);
+        for (int m = 0; m < M; m++) {
+            const bool mine = MODE == kModeMfma ? (m >> 2) % 4 == j : j == 0;
+            if (mine) lds[(wave * M + m) * 16 + r] = res[m];
+        }
+        __syncthreads();
+        if (part == 0) {
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                float v = 0.0f;
+                for (int w = 1; w < KS; w++) v += lds[((wave + w) * M + m) * 16 + r];
+                res[m] += v;
+            }
+        }
+    }
+    if (part == 0 && row < rows) {
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const bool mine = MODE == kModeMfma ? (m >> 2) % 4 == j : j == 0;
+            if (mine && m < a.mcount) {
+                float v = res[m];
+                if constexpr (F::FMT == TITAN_NVFP4) v *= W.gscale;
+                if constexpr (F::FMT == TITAN_FP8_E4M3) v *= ((const float*)W.scales)[row];
+                store_out(P.y, (int64_t)(a.m0 + m) * P.ldy + row, a.ydt, v);
+            }
         }
     }
 }
 
-// ---- generic fallback for ragged REF shapes: one workgroup per row -------------
+// ---- generic fallback for shapes the fast kernel does not take ------------------
 template <int FMT, int M>
 __global__ __launch_bounds__(256) void qgemv_generic_kernel(GemvArgs a) {
     __shared__ float red[M][4];
@@ -289,7 +280,8 @@ __global__ __launch_bounds__(256) void qgemv_generic_kernel(GemvArgs a) {
     for (int c = threadIdx.x; c < W.g.cols; c += 256) {
         float w = elem<FMT, TITAN_LAYOUT_REF>(W, row, c);
 #pragma unroll
-        for (int m = 0; m < M; m++) acc[m] += w * load_act(P.x, (int64_t)(a.m0 + m) * P.ldx + c, a.xdt);
+        for (int m = 0; m < M; m++)
+            if (m < a.mcount) acc[m] += w * load_act(P.x, (int64_t)(a.m0 + m) * P.ldx + c, a.xdt);
     }
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
@@ -298,7 +290,7 @@ __global__ __launch_bounds__(256) void qgemv_generic_kernel(GemvArgs a) {
         if (lane == 0) red[m][wave] = v;
     }
     __syncthreads();
-    if (threadIdx.x < M) {
+    if (threadIdx.x < a.mcount && threadIdx.x < M) {
         const int m = threadIdx.x;
         float v = red[m][0] + red[m][1] + red[m][2] + red[m][3];
         store_out(P.y, (int64_t)(a.m0 + m) * P.ldy + row, a.ydt, v);
@@ -316,107 +308,142 @@ __global__ __launch_bounds__(256) void qdequant_kernel(WDesc w, void* out, int o
     }
 }
 
-}  // namespace tq
-
-
-namespace tq {
+// ============================================================================
+// launchers
+// ============================================================================
 template <int FMT, int LAYOUT> struct Pick;
-template <int L> struct Pick<TITAN_INT4, L> { using type = FmtInt4<L>; };
-template <int L> struct Pick<TITAN_INT2, L> { using type = FmtInt2<L>; };
-template <int L> struct Pick<TITAN_FP4, L> { using type = FmtFp4<L>; };
-template <int L> struct Pick<TITAN_NVFP4, L> { using type = FmtNvfp4<L>; };
-template <int L> struct Pick<TITAN_Q4_K, L> { using type = FmtQ4K<L>; };
-template <int L> struct Pick<TITAN_Q3_K, L> { using type = FmtQ3K<L>; };
-template <int L> struct Pick<TITAN_FP8_E4M3, L> { using type = FmtFp8<L>; };
+template <int L> struct Pick<TITAN_INT4, L> { using type = FxInt4<L>; };
+template <int L> struct Pick<TITAN_INT2, L> { using type = FxInt2<L>; };
+template <int L> struct Pick<TITAN_FP4, L> { using type = FxFp4<L>; };
+template <int L> struct Pick<TITAN_NVFP4, L> { using type = FxNvfp4<L>; };
+template <int L> struct Pick<TITAN_Q4_K, L> { using type = FxQ4K<L>; };
+template <int L> struct Pick<TITAN_Q3_K, L> { using type = FxQ3K<L>; };
+template <int L> struct Pick<TITAN_FP8_E4M3, L> { using type = FxFp8<L>; };
 
-template <class F, int M, bool HX>
-void launch_fast_m(GemvArgs& a, int total_tiles, hipStream_t st) {
-    // Four row tiles per workgroup for large problems (and for many tokens,
-    // which keeps the activation stage small); one tile otherwise.
-    const int rt = (total_tiles >= 4 * 1024 || M > 4) ? 4 : 1;
-    // phase width: whole groups of chunks, at most kGemvLdsBytes of staged
-    // activations (fp32, or fp16 + per-16 sums), at least one group, no
-    // wider than the longest row
-    const int step = kGemvWaves * (4 / rt) * F::CHUNK_COLS;
+template <class F, int M, int MODE>
+void launch_mode(GemvArgs& a, int, hipStream_t st) {
+    const int gsteps = a.p[0].gsteps;  // MFMA: word steps per scale group (same for all problems)
+    // K split per problem so that every wave folds a similar number of
+    // chunks (long rows are shared by 2 or 4 waves)
+    // (target: about 2048 waves in flight, at least 8 chunks per wave)
+    long long work = 0;
+    for (int i = 0; i < a.n; i++) work += (long long)a.p[i].ntiles * a.p[i].nchunks;
+    const long long target = work / 2048 > 8 ? work / 2048 : 8;
+    for (int i = 0; i < a.n; i++) {
+        int ks = 0;
+        while (ks < 2 && a.p[i].nchunks > target << ks) ks++;
+        a.p[i].ks_log = ks;
+    }
+    // phase width: whole rounds of 4 waves x U = 4 chunks, at most
+    // kGemvLdsBytes of staged activations (at least one round), no wider
+    // than the longest row
+    const int step = 16 * F::CHUNK_COLS;
     int maxcols = 0;
     for (int i = 0; i < a.n; i++) maxcols = maxcols > a.p[i].w.g.cols ? maxcols : a.p[i].w.g.cols;
-    const int per_col_x4 = HX ? 9 : 16;  // 4 x bytes per column per token
-    int cap = (kGemvLdsBytes * 4 / per_col_x4 / M) / step * step;
+    // bytes per column per token, x4: fp32 + sums 17, fp16 + sums 9, fp16 8
+    const int per4 = MODE == kModeF32 ? 17 : MODE == kModeDot2 ? 9 : 8;
+    int cap = (kGemvLdsBytes * 4 / per4 / M) / step * step;
     if (cap < step) cap = step;
-    int need = (maxcols + step - 1) / step * step;
+    const int need = (maxcols + step - 1) / step * step;
     a.pc = need < cap ? need : cap;
-    const size_t stage = (size_t)M * a.pc * per_col_x4 / 4;
-    const size_t red = (size_t)kGemvWaves * rt * M * 16 * 4;
+    const size_t stage = (size_t)M * a.pc * per4 / 4 + 16;
+    const size_t red = (size_t)kGemvWaves * M * 16 * 4;
     const size_t lds = stage > red ? stage : red;
+    // workgroups: long-K problems first (they take longest)
+    int order[TITAN_MAX_BATCH];
+    for (int i = 0; i < a.n; i++) order[i] = i;
+    for (int i = 1; i < a.n; i++)
+        for (int k2 = i; k2 > 0 && a.p[order[k2]].nchunks > a.p[order[k2 - 1]].nchunks; k2--) {
+            int t = order[k2]; order[k2] = order[k2 - 1]; order[k2 - 1] = t;
+        }
+    GemvArgs b = a;
     int wg = 0;
     for (int i = 0; i < a.n; i++) {
-        a.p[i].wg_begin = wg;
-        wg += (a.p[i].ntiles + rt - 1) / rt;
+        b.p[i] = a.p[order[i]];
+        b.p[i].wg_begin = wg;
+        wg += (b.p[i].ntiles + (kGemvWaves >> b.p[i].ks_log) - 1) / (kGemvWaves >> b.p[i].ks_log);
     }
-    if (rt == 4)
-        hipLaunchKernelGGL((qgemv_kernel<F, M, 4, HX>), dim3(wg), dim3(kGemvThreads), lds, st, a);
-    else
-        hipLaunchKernelGGL((qgemv_kernel<F, M, 1, HX>), dim3(wg), dim3(kGemvThreads), lds, st, a);
+    if constexpr (MODE == kModeMfma) {
+        if (gsteps == 4)
+            hipLaunchKernelGGL((qgemv_kernel<F, M, MODE, 4>), dim3(wg), dim3(kGemvThreads), lds, st, b);
+        else if (gsteps == 2)
+            hipLaunchKernelGGL((qgemv_kernel<F, M, MODE, 2>), dim3(wg), dim3(kGemvThreads), lds, st, b);
+        else
+            hipLaunchKernelGGL((qgemv_kernel<F, M, MODE, 1>), dim3(wg), dim3(kGemvThreads), lds, st, b);
+    } else {
+        constexpr bool grouped = F::FMT == TITAN_INT4 || F::FMT == TITAN_INT2 || F::FMT == TITAN_FP4;
+        if (grouped && gsteps == 1)
+            hipLaunchKernelGGL((qgemv_kernel<F, M, MODE, 1>), dim3(wg), dim3(kGemvThreads), lds, st, b);
+        else if (grouped && gsteps == 2)
+            hipLaunchKernelGGL((qgemv_kernel<F, M, MODE, 2>), dim3(wg), dim3(kGemvThreads), lds, st, b);
+        else
+            hipLaunchKernelGGL((qgemv_kernel<F, M, MODE, 4>), dim3(wg), dim3(kGemvThreads), lds, st, b);
+    }
 }
 
-template <class F, int M>
-void launch_fast_m(GemvArgs& a, int total_tiles, hipStream_t st) {
-    // fp16 activations with 16-byte aligned rows take the packed fp16 path
-    bool hx = a.xdt == TITAN_FP16;
-    for (int i = 0; i < a.n; i++)
-        hx = hx && ((uintptr_t)a.p[i].x & 15) == 0 && (a.p[i].ldx & 7) == 0;
-    if (hx) launch_fast_m<F, M, true>(a, total_tiles, st);
-    else launch_fast_m<F, M, false>(a, total_tiles, st);
-}
-
+// Launches tokens [a.m0, a.m0 + mcount) (mcount <= 8 for the VALU modes, <= 32
+// for MFMA).
 template <class F>
-void launch_fast(GemvArgs& a, int mcount, int total_tiles, hipStream_t st) {
+void launch_fast(GemvArgs& a, int mcount, int mode, int total_tiles, hipStream_t st) {
     a.mcount = mcount;
-    if (mcount == 1) launch_fast_m<F, 1>(a, total_tiles, st);
-    else if (mcount == 2) launch_fast_m<F, 2>(a, total_tiles, st);
-    else if (mcount <= 4) launch_fast_m<F, 4>(a, total_tiles, st);
-    else launch_fast_m<F, 8>(a, total_tiles, st);
+    if (mode == kModeMfma) {
+        if constexpr (F::HAS_MFMA) {
+            if (mcount == 1) launch_mode<F, 1, kModeMfma>(a, total_tiles, st);
+            else if (mcount == 2) launch_mode<F, 2, kModeMfma>(a, total_tiles, st);
+            else if (mcount <= 4) launch_mode<F, 4, kModeMfma>(a, total_tiles, st);
+            else if (mcount <= 8) launch_mode<F, 8, kModeMfma>(a, total_tiles, st);
+            else if (mcount <= 16) launch_mode<F, 16, kModeMfma>(a, total_tiles, st);
+            else launch_mode<F, 32, kModeMfma>(a, total_tiles, st);
+        }
+    } else if (mode == kModeDot2) {
+        if (mcount == 1) launch_mode<F, 1, kModeDot2>(a, total_tiles, st);
+        else if (mcount == 2) launch_mode<F, 2, kModeDot2>(a, total_tiles, st);
+        else if (mcount <= 4) launch_mode<F, 4, kModeDot2>(a, total_tiles, st);
+        else launch_mode<F, 8, kModeDot2>(a, total_tiles, st);
+    } else {
+        if (mcount == 1) launch_mode<F, 1, kModeF32>(a, total_tiles, st);
+        else if (mcount == 2) launch_mode<F, 2, kModeF32>(a, total_tiles, st);
+        else if (mcount <= 4) launch_mode<F, 4, kModeF32>(a, total_tiles, st);
+        else launch_mode<F, 8, kModeF32>(a, total_tiles, st);
+    }
 }
 
 template <int FMT>
 void launch_generic(GemvArgs& a, int mcount, int rows, hipStream_t st) {
-    switch (mcount) {
-#define TQ_G(MM) \
-    case MM: hipLaunchKernelGGL((qgemv_generic_kernel<FMT, MM>), dim3(rows), dim3(256), 0, st, a); break;
-        TQ_G(1) TQ_G(2) TQ_G(3) TQ_G(4) TQ_G(5) TQ_G(6) TQ_G(7)
-        default: hipLaunchKernelGGL((qgemv_generic_kernel<FMT, 8>), dim3(rows), dim3(256), 0, st, a); break;
-#undef TQ_G
+    a.mcount = mcount;
+    if (mcount == 1) hipLaunchKernelGGL((qgemv_generic_kernel<FMT, 1>), dim3(rows), dim3(256), 0, st, a);
+    else if (mcount <= 4) hipLaunchKernelGGL((qgemv_generic_kernel<FMT, 4>), dim3(rows), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((qgemv_generic_kernel<FMT, 8>), dim3(rows), dim3(256), 0, st, a);
+}
+
+template <int FMT>
+void dispatch_fmt(GemvArgs& a, int layout, int mcount, int mode, int total_tiles, hipStream_t st) {
+    if (layout == TITAN_LAYOUT_TILED) {
+        launch_fast<typename Pick<FMT, TITAN_LAYOUT_TILED>::type>(a, mcount, mode, total_tiles, st);
+    } else {
+        if constexpr (FMT != TITAN_Q3_K)
+            launch_fast<typename Pick<FMT, TITAN_LAYOUT_REF>::type>(a, mcount, mode, total_tiles, st);
     }
 }
 
 template <int FMT>
-void dispatch_fmt(GemvArgs& a, int layout, bool fast, int mcount, int total_tiles, hipStream_t st) {
-    if (!fast) {
-        launch_generic<FMT>(a, mcount, a.p[0].w.g.rows, st);
-    } else if (layout == TITAN_LAYOUT_TILED) {
-        launch_fast<typename Pick<FMT, TITAN_LAYOUT_TILED>::type>(a, mcount, total_tiles, st);
-    } else {
-        if constexpr (FMT != TITAN_Q3_K)
-            launch_fast<typename Pick<FMT, TITAN_LAYOUT_REF>::type>(a, mcount, total_tiles, st);
-    }
-}
+bool fmt_has_mfma() { return Pick<FMT, TITAN_LAYOUT_TILED>::type::HAS_MFMA; }
 
 }  // namespace tq
 
 // One translation unit per format instantiates the launchers (parallel build).
 namespace tq {
-void dispatch_gemv_int4(GemvArgs& a, int layout, int mcount, int total_tiles, hipStream_t st);
-void dispatch_gemv_generic_int4(GemvArgs& a, int mcount, int rows, hipStream_t st);
-void dispatch_gemv_int2(GemvArgs& a, int layout, int mcount, int total_tiles, hipStream_t st);
-void dispatch_gemv_generic_int2(GemvArgs& a, int mcount, int rows, hipStream_t st);
-void dispatch_gemv_fp4(GemvArgs& a, int layout, int mcount, int total_tiles, hipStream_t st);
-void dispatch_gemv_generic_fp4(GemvArgs& a, int mcount, int rows, hipStream_t st);
-void dispatch_gemv_nvfp4(GemvArgs& a, int layout, int mcount, int total_tiles, hipStream_t st);
-void dispatch_gemv_generic_nvfp4(GemvArgs& a, int mcount, int rows, hipStream_t st);
-void dispatch_gemv_q4k(GemvArgs& a, int layout, int mcount, int total_tiles, hipStream_t st);
-void dispatch_gemv_generic_q4k(GemvArgs& a, int mcount, int rows, hipStream_t st);
-void dispatch_gemv_q3k(GemvArgs& a, int layout, int mcount, int total_tiles, hipStream_t st);
-void dispatch_gemv_generic_q3k(GemvArgs& a, int mcount, int rows, hipStream_t st);
-void dispatch_gemv_fp8(GemvArgs& a, int layout, int mcount, int total_tiles, hipStream_t st);
-void dispatch_gemv_generic_fp8(GemvArgs& a, int mcount, int rows, hipStream_t st);
+#define TQ_DECL(name)                                                                              \
+    void dispatch_gemv_##name(GemvArgs& a, int layout, int mcount, int mode, int total_tiles,       \
+                              hipStream_t st);                                                     \
+    void dispatch_gemv_generic_##name(GemvArgs& a, int mcount, int rows, hipStream_t st);          \
+    bool gemv_has_mfma_##name();
+TQ_DECL(int4)
+TQ_DECL(int2)
+TQ_DECL(fp4)
+TQ_DECL(nvfp4)
+TQ_DECL(q4k)
+TQ_DECL(q3k)
+TQ_DECL(fp8)
+#undef TQ_DECL
 }  // namespace tq

@@ -5,11 +5,15 @@
 //
 // TILED layout (one buffer, all planes back to back, same byte count as REF):
 //   code plane   row r's code bytes (K-quants: the concatenated qs arrays of
-//                its blocks) cut into 64-byte chunks; tile t = rows 16t..16t+15;
-//                chunk c of tile t is 1 KiB at ((t*nchunks + c) * 64 + lane) * 16
-//                with lane = 16*j + (r % 16) holding bytes [64c + 16j, +16) of
-//                row r.  A wave's 64 lanes read one chunk of 16 rows as 1 KiB
-//                of contiguous memory.
+//                its blocks) cut into 64-byte chunks of 16 words; tile t = rows
+//                16t..16t+15; chunk c of tile t is 1 KiB at
+//                ((t*nchunks + c) * 64 + lane) * 16, lane = 16*j + (r % 16)
+//                holding words j, 4+j, 8+j, 12+j of row r's chunk (word i of
+//                the lane = chunk bytes [16i + 4j, +4)).  A wave's 64 lanes
+//                read one chunk of 16 rows as 1 KiB of contiguous memory, and
+//                word i of the four lanes of a row covers chunk bytes
+//                [16i, 16i + 16): one matrix-core k-step over contiguous
+//                columns.
 //   aux planes   per format, also 16-row interleaved (see tiled_* below).
 #pragma once
 
@@ -70,6 +74,11 @@ TQ_HD size_t tiled_code_off(const Geo& g, int row, int chunk, int j) {
 TQ_HD size_t tiled_code_plane_bytes(const Geo& g) {
     return (size_t)g.rows * g.row_code_bytes;
 }
+// Offset of byte b (0 <= b < row_code_bytes) of row `row`'s code bytes.
+TQ_HD size_t tiled_code_byte(const Geo& g, int row, int b) {
+    const int c = b >> 6, w = (b & 63) >> 2;
+    return tiled_code_off(g, row, c, w & 3) + 4 * (w >> 2) + (b & 3);
+}
 
 // ---- TILED aux planes (offsets from the start of the buffer) ----------------
 // INT4 / INT2: u32 (scale | bias << 16) at [t][group][r].
@@ -82,21 +91,21 @@ TQ_HD size_t tiled_fp4s_off(const Geo& g, int row, int grp) {
     return tiled_code_plane_bytes(g) +
            (((size_t)(row >> 4) * g.ngroups + grp) * 16 + (row & 15)) * 2;
 }
-// NVFP4: u16 (two e4m3 scales of slot j of chunk c) at [t][c][j][r].
-TQ_HD size_t tiled_nvs_off(const Geo& g, int row, int chunk, int j) {
+// NVFP4: the 8 e4m3 scales of chunk c (128 columns) at [t][c][r] (8 bytes).
+TQ_HD size_t tiled_nvs_off(const Geo& g, int row, int chunk) {
     return tiled_code_plane_bytes(g) +
-           ((((size_t)(row >> 4) * g.nchunks + chunk) * 4 + j) * 16 + (row & 15)) * 2;
+           (((size_t)(row >> 4) * g.nchunks + chunk) * 16 + (row & 15)) * 8;
 }
 // Q4_K: 16-byte block header {d, dmin, scales[12]} at [t][blk][r].
 TQ_HD size_t tiled_q4k_hdr_off(const Geo& g, int row, int blk) {
     return tiled_code_plane_bytes(g) +
            (((size_t)(row >> 4) * g.nblk + blk) * 16 + (row & 15)) * 16;
 }
-// Q3_K: hmask halves (16 B) at [t][blk][hh][r]; scales (12 B) at [t][blk][r];
-// d (2 B) at [t][blk][r].
-TQ_HD size_t tiled_q3k_hmask_off(const Geo& g, int row, int blk, int hh) {
+// Q3_K: hmask words (j, 4+j) (8 B) at [t][blk][j][r]; scales (12 B) at
+// [t][blk][r]; d (2 B) at [t][blk][r].
+TQ_HD size_t tiled_q3k_hmask_off(const Geo& g, int row, int blk, int j) {
     return tiled_code_plane_bytes(g) +
-           ((((size_t)(row >> 4) * g.nblk + blk) * 2 + hh) * 16 + (row & 15)) * 16;
+           ((((size_t)(row >> 4) * g.nblk + blk) * 4 + j) * 16 + (row & 15)) * 8;
 }
 TQ_HD size_t tiled_q3k_sc_off(const Geo& g, int row, int blk) {
     return tiled_code_plane_bytes(g) + (size_t)g.rows * g.nblk * 32 +
@@ -109,33 +118,41 @@ TQ_HD size_t tiled_q3k_d_off(const Geo& g, int row, int blk) {
 
 // Total bytes of the TILED buffer, or 0 if the format/shape has no tiled
 // form.  Tiled weights are always served by the fast GEMV kernel, so the
-// group size must also keep each lane's 16-byte slot inside one group.
+// group size must also be a power of two that keeps each lane's 16-byte slot
+// inside one group, and the buffer must stay below 4 GiB.
 TQ_HD size_t tiled_total_bytes(int fmt, int rows, int cols, int gs) {
     if (rows <= 0 || cols <= 0 || (rows & 15)) return 0;
     Geo g = make_geo(fmt, rows, cols, gs);
     if (!g.row_code_bytes || (g.row_code_bytes & 63)) return 0;
     size_t codes = tiled_code_plane_bytes(g);
+    // groups: a power of two no smaller than one lane's 16-byte slot
+    const bool gs_ok = gs > 0 && cols % gs == 0 && gs % g.slot_cols == 0 && (gs & (gs - 1)) == 0;
+    size_t total = 0;
     switch (fmt) {
         case TITAN_INT4:
         case TITAN_INT2:
-            if (gs <= 0 || cols % gs || gs % g.slot_cols) return 0;
-            return codes + (size_t)rows * g.ngroups * 4;
+            if (gs_ok) total = codes + (size_t)rows * g.ngroups * 4;
+            break;
         case TITAN_FP4:
-            if (gs <= 0 || cols % gs || gs % g.slot_cols) return 0;
-            return codes + (size_t)rows * g.ngroups * 2;
+            if (gs_ok) total = codes + (size_t)rows * g.ngroups * 2;
+            break;
         case TITAN_NVFP4:
-            return codes + (size_t)rows * (cols / 16);
+            if (cols % 128 == 0) total = codes + (size_t)rows * (cols / 16);
+            break;
         case TITAN_Q4_K:
-            if (cols % 256) return 0;
-            return codes + (size_t)rows * g.nblk * 16;
+            if (cols % 256 == 0) total = codes + (size_t)rows * g.nblk * 16;
+            break;
         case TITAN_Q3_K:
-            if (cols % 256) return 0;
-            return codes + (size_t)rows * g.nblk * 46;
+            if (cols % 256 == 0) total = codes + (size_t)rows * g.nblk * 46;
+            break;
         case TITAN_FP8_E4M3:
-            return codes;
+            total = codes;
+            break;
         default:
-            return 0;
+            break;
     }
+    // the kernels address the buffer with 32-bit per-lane offsets
+    return total < (1ull << 32) ? total : 0;
 }
 
 }  // namespace tq

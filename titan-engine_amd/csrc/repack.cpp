@@ -62,9 +62,8 @@ extern "C" int titan_repack_host(int fmt, int rows, int cols, int gs, const void
     RefRowCodes rc(g, codes);
     for (int r = 0; r < rows; r++) {
         const uint8_t* src = rc.row(r);
-        for (int c = 0; c < g.nchunks; c++)
-            for (int j = 0; j < 4; j++)
-                memcpy(out + tq::tiled_code_off(g, r, c, j), src + c * 64 + j * 16, 16);
+        for (int b = 0; b < g.row_code_bytes; b += 4)
+            memcpy(out + tq::tiled_code_byte(g, r, b), src + b, 4);
     }
     const uint16_t* s16 = (const uint16_t*)scales;
     const uint16_t* b16 = (const uint16_t*)biases;
@@ -86,9 +85,7 @@ extern "C" int titan_repack_host(int fmt, int rows, int cols, int gs, const void
                 break;
             case TITAN_NVFP4:
                 for (int c = 0; c < g.nchunks; c++)
-                    for (int j = 0; j < 4; j++)
-                        memcpy(out + tq::tiled_nvs_off(g, r, c, j),
-                               s8 + (size_t)r * (cols / 16) + c * 8 + 2 * j, 2);
+                    memcpy(out + tq::tiled_nvs_off(g, r, c), s8 + (size_t)r * (cols / 16) + c * 8, 8);
                 break;
             case TITAN_Q4_K:
                 for (int b = 0; b < g.nblk; b++)
@@ -98,8 +95,10 @@ extern "C" int titan_repack_host(int fmt, int rows, int cols, int gs, const void
             case TITAN_Q3_K:
                 for (int b = 0; b < g.nblk; b++) {
                     const uint8_t* blk = blocks + ((size_t)r * g.nblk + b) * 110;
-                    memcpy(out + tq::tiled_q3k_hmask_off(g, r, b, 0), blk, 16);
-                    memcpy(out + tq::tiled_q3k_hmask_off(g, r, b, 1), blk + 16, 16);
+                    for (int j = 0; j < 4; j++) {
+                        memcpy(out + tq::tiled_q3k_hmask_off(g, r, b, j), blk + 4 * j, 4);
+                        memcpy(out + tq::tiled_q3k_hmask_off(g, r, b, j) + 4, blk + 16 + 4 * j, 4);
+                    }
                     memcpy(out + tq::tiled_q3k_sc_off(g, r, b), blk + 96, 12);
                     memcpy(out + tq::tiled_q3k_d_off(g, r, b), blk + 108, 2);
                 }
@@ -125,9 +124,8 @@ extern "C" int titan_unpack_host(int fmt, int rows, int cols, int gs, const void
     uint8_t* c8 = (uint8_t*)codes;
     std::vector<uint8_t> row((size_t)g.row_code_bytes);
     for (int r = 0; r < rows; r++) {
-        for (int c = 0; c < g.nchunks; c++)
-            for (int j = 0; j < 4; j++)
-                memcpy(&row[(size_t)c * 64 + j * 16], in + tq::tiled_code_off(g, r, c, j), 16);
+        for (int b = 0; b < g.row_code_bytes; b += 4)
+            memcpy(&row[(size_t)b], in + tq::tiled_code_byte(g, r, b), 4);
         if (fmt == TITAN_Q4_K || fmt == TITAN_Q3_K) {
             int bb = tq::kquant_block_bytes(fmt), qsb = fmt == TITAN_Q4_K ? 128 : 64,
                 qso = fmt == TITAN_Q4_K ? 16 : 32;
@@ -157,9 +155,7 @@ extern "C" int titan_unpack_host(int fmt, int rows, int cols, int gs, const void
                 break;
             case TITAN_NVFP4:
                 for (int c = 0; c < g.nchunks; c++)
-                    for (int j = 0; j < 4; j++)
-                        memcpy(s8 + (size_t)r * (cols / 16) + c * 8 + 2 * j,
-                               in + tq::tiled_nvs_off(g, r, c, j), 2);
+                    memcpy(s8 + (size_t)r * (cols / 16) + c * 8, in + tq::tiled_nvs_off(g, r, c), 8);
                 break;
             case TITAN_Q4_K:
                 for (int b = 0; b < g.nblk; b++)
@@ -168,8 +164,10 @@ extern "C" int titan_unpack_host(int fmt, int rows, int cols, int gs, const void
             case TITAN_Q3_K:
                 for (int b = 0; b < g.nblk; b++) {
                     uint8_t* blk = c8 + ((size_t)r * g.nblk + b) * 110;
-                    memcpy(blk, in + tq::tiled_q3k_hmask_off(g, r, b, 0), 16);
-                    memcpy(blk + 16, in + tq::tiled_q3k_hmask_off(g, r, b, 1), 16);
+                    for (int j = 0; j < 4; j++) {
+                        memcpy(blk + 4 * j, in + tq::tiled_q3k_hmask_off(g, r, b, j), 4);
+                        memcpy(blk + 16 + 4 * j, in + tq::tiled_q3k_hmask_off(g, r, b, j) + 4, 4);
+                    }
                     memcpy(blk + 96, in + tq::tiled_q3k_sc_off(g, r, b), 12);
                     memcpy(blk + 108, in + tq::tiled_q3k_d_off(g, r, b), 2);
                 }
