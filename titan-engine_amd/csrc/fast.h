@@ -14,7 +14,7 @@
 //    v_dot2_f32_f16 multiplies it with an activation pair.  Activations sit
 //    in LDS permuted per format (stage8) so one 128-bit read yields the
 //    pairs that line up with the masked code pairs.
-//  * fold_mfma (fp16 activations, selected formats): the same fp16 code
+//  * issue / finish (fp16 activations, selected formats): the same fp16 code
 //    operands feed v_mfma_f32_16x16x{16,32}_f16 with activations as the A
 //    operand (16 tokens x k) and codes as B (k x 16 rows); lane (r, q) of the
 //    accumulator holds row r, tokens 4q..4q+3, so the lane's own per-row
@@ -222,45 +222,58 @@ struct FxNib {
     }
     // MFMA: per step one 16x16x32 for sum(q*x) and one against ones for
     // sum(x); folded into acc at the end of each group.
-    template <int NB, int NV, int GS>
-    TQ_DEV static void fold_mfma(const Raw& r, const Dec& d, int j, const _Float16* const* xt,
-                                 f4_t* acc) {
-#ifdef TQ_EXP_NOFOLD
-        acc[0][0] += __builtin_bit_cast(float, (r.w[0] ^ r.w[1] ^ r.w[2] ^ r.w[3]) & 0x3FFFFFFF) +
-                     d.s[3] + (float)xt[0][8 * j];
-        return;
-#endif
+    // MFMA, two stages so that a chunk's MFMAs are in flight while the
+    // previous chunk is scaled: issue() runs the MFMAs of every scale group
+    // of the chunk (codes low / high nibble, and the activation sums against
+    // ones unless SX), finish() applies the per-row scales.  SX: sum(x) per
+    // 32 columns comes from LDS instead (M <= 4: only accumulator entries of
+    // lanes q = 0 hold tokens).
+    template <int NB, int GS, bool SX>
+    struct Tmp { f4_t C[4 / GS][NB], H[4 / GS][NB], O[SX ? 1 : 4 / GS][NB]; };
+    template <int NB, int GS, bool SX>
+    TQ_DEV static void issue(const Raw& r, int j, const _Float16* const* xt, Tmp<NB, GS, SX>& T) {
         const h8_t ones = h8_of(make_uint4(kOnes2, kOnes2, kOnes2, kOnes2));
-        f4_t C[NB], H[NB], O[NB];
-#pragma unroll
-        for (int n = 0; n < NB; n++) { C[n] = f4_zero(); H[n] = f4_zero(); O[n] = f4_zero(); }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
+            const int g = i / GS;
             const uint32_t w = r.w[i], u = w >> 8;
             const h4_t blo = h4_of(w & 0x000F000Fu, u & 0x000F000Fu);  // (n0, n4, n2, n6)
             const h4_t bhi = h4_of(w & 0x00F000F0u, u & 0x00F000F0u);  // (n1, n5, n3, n7) x16
 #pragma unroll
             for (int n = 0; n < NB; n++) {
                 const uint4 xv = *(const uint4*)(xt[n] + 32 * i + 8 * j);
-                C[n] = mfma16(h4_of(xv.x, xv.y), blo, C[n]);
-                H[n] = mfma16(h4_of(xv.z, xv.w), bhi, H[n]);
-                O[n] = mfma32(h8_of(xv), ones, O[n]);
+                const bool first = i % GS == 0;
+                T.C[g][n] = mfma16(h4_of(xv.x, xv.y), blo, first ? f4_zero() : T.C[g][n]);
+                T.H[g][n] = mfma16(h4_of(xv.z, xv.w), bhi, first ? f4_zero() : T.H[g][n]);
+                if constexpr (!SX) T.O[g][n] = mfma32(h8_of(xv), ones, first ? f4_zero() : T.O[g][n]);
             }
-            if ((i + 1) % GS == 0) {  // end of a group
-                const float s = d.s[i] * kTwo24, sh = d.s[i] * (kTwo24 / 16.0f), bb = d.b[i];
+        }
+    }
+    template <int NB, int NV, int GS, bool SX>
+    TQ_DEV static void finish(const Tmp<NB, GS, SX>& T, const Dec& d, const float* sx, f4_t* acc) {
 #pragma unroll
-                for (int n = 0; n < NB; n++) {
+        for (int g = 0; g < 4 / GS; g++) {
+            const int i = g * GS;
+            const float s = d.s[i] * kTwo24, sh = d.s[i] * (kTwo24 / 16.0f), bb = d.b[i];
+            float4 xs;
+            if constexpr (SX) {  // sums of the group's columns for tokens 0..3
+                xs = *(const float4*)(sx + 4 * i);
 #pragma unroll
-                    for (int v = 0; v < NV; v++) {
-                        float t = __builtin_fmaf(s, C[n][v], acc[n][v]);
-                        t = __builtin_fmaf(sh, H[n][v], t);
-                        acc[n][v] = __builtin_fmaf(bb, O[n][v], t);
-                    }
-                    C[n] = f4_zero();
-                    H[n] = f4_zero();
-                    O[n] = f4_zero();
+                for (int q = 1; q < GS; q++) {
+                    const float4 t = *(const float4*)(sx + 4 * (i + q));
+                    xs.x += t.x; xs.y += t.y; xs.z += t.z; xs.w += t.w;
                 }
             }
+#pragma unroll
+            for (int n = 0; n < NB; n++)
+#pragma unroll
+                for (int v = 0; v < NV; v++) {
+                    float t = __builtin_fmaf(s, T.C[g][n][v], acc[n][v]);
+                    t = __builtin_fmaf(sh, T.H[g][n][v], t);
+                    const float o = SX ? (v == 0 ? xs.x : v == 1 ? xs.y : v == 2 ? xs.z : xs.w)
+                                       : T.O[SX ? 0 : g][n][v];
+                    acc[n][v] = __builtin_fmaf(bb, o, t);
+                }
         }
     }
     // 8 staged activations starting at chunk column d0 (d0 % 8 == 0)
@@ -380,15 +393,14 @@ struct FxInt2 {
         }
         return j == 0 ? t + bias(d, s16) : t;
     }
-    template <int NB, int NV, int GS>
-    TQ_DEV static void fold_mfma(const Raw& r, const Dec& d, int j, const _Float16* const* xt,
-                                 f4_t* acc) {
+    template <int NB, int GS, bool SX>
+    struct Tmp { f4_t C[4 / GS][NB], O[SX ? 1 : 4 / GS][NB]; };
+    template <int NB, int GS, bool SX>
+    TQ_DEV static void issue(const Raw& r, int j, const _Float16* const* xt, Tmp<NB, GS, SX>& T) {
         const h8_t ones = h8_of(make_uint4(kOnes2, kOnes2, kOnes2, kOnes2));
-        f4_t C[NB], O[NB];
-#pragma unroll
-        for (int n = 0; n < NB; n++) { C[n] = f4_zero(); O[n] = f4_zero(); }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
+            const int g = i / GS;
             const uint32_t w = r.w[i];
             // fields k = 0..3 of w and w >> 8, each shifted down to bit 0
             const h8_t b0 = h8_of(make_uint4(w & 0x00030003u, (w >> 8) & 0x00030003u,
@@ -398,26 +410,41 @@ struct FxInt2 {
 #pragma unroll
             for (int n = 0; n < NB; n++) {
                 const _Float16* p = xt[n] + 64 * i + 16 * j;
-                const uint4 xa = *(const uint4*)p;
-                const uint4 xb = *(const uint4*)(p + 8);
-                C[n] = mfma32(h8_of(xa), b0, C[n]);
-                C[n] = mfma32(h8_of(xb), b1, C[n]);
-                O[n] = mfma32(h8_of(xa), ones, O[n]);
-                O[n] = mfma32(h8_of(xb), ones, O[n]);
-            }
-            if ((i + 1) % GS == 0) {
-                const float s = d.s[i] * kTwo24, bb = d.b[i];
-#pragma unroll
-                for (int n = 0; n < NB; n++) {
-#pragma unroll
-                    for (int v = 0; v < NV; v++) {
-                        acc[n][v] = __builtin_fmaf(s, C[n][v], acc[n][v]);
-                        acc[n][v] = __builtin_fmaf(bb, O[n][v], acc[n][v]);
-                    }
-                    C[n] = f4_zero();
-                    O[n] = f4_zero();
+                const uint4 xa = *(const uint4*)p, xb = *(const uint4*)(p + 8);
+                const bool first = i % GS == 0;
+                T.C[g][n] = mfma32(h8_of(xa), b0, first ? f4_zero() : T.C[g][n]);
+                T.C[g][n] = mfma32(h8_of(xb), b1, T.C[g][n]);
+                if constexpr (!SX) {
+                    T.O[g][n] = mfma32(h8_of(xa), ones, first ? f4_zero() : T.O[g][n]);
+                    T.O[g][n] = mfma32(h8_of(xb), ones, T.O[g][n]);
                 }
             }
+        }
+    }
+    template <int NB, int NV, int GS, bool SX>
+    TQ_DEV static void finish(const Tmp<NB, GS, SX>& T, const Dec& d, const float* sx, f4_t* acc) {
+#pragma unroll
+        for (int g = 0; g < 4 / GS; g++) {
+            const int i = g * GS;
+            const float s = d.s[i] * kTwo24, bb = d.b[i];
+            float4 xs;
+            if constexpr (SX) {  // a word step is 64 columns: two 32-column sums
+                xs = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int q = 0; q < 2 * GS; q++) {
+                    const float4 t = *(const float4*)(sx + 4 * (2 * i + q));
+                    xs.x += t.x; xs.y += t.y; xs.z += t.z; xs.w += t.w;
+                }
+            }
+#pragma unroll
+            for (int n = 0; n < NB; n++)
+#pragma unroll
+                for (int v = 0; v < NV; v++) {
+                    const float t = __builtin_fmaf(s, T.C[g][n][v], acc[n][v]);
+                    const float o = SX ? (v == 0 ? xs.x : v == 1 ? xs.y : v == 2 ? xs.z : xs.w)
+                                       : T.O[SX ? 0 : g][n][v];
+                    acc[n][v] = __builtin_fmaf(bb, o, t);
+                }
         }
     }
     TQ_DEV static uint4 stage8(const _Float16* xr, int d0) {
@@ -509,8 +536,11 @@ struct FxNvfp4 {
         }
         return t * kTwo14;
     }
-    template <int NB, int NV, int GS>
-    TQ_DEV static void fold_mfma(const Raw&, const Dec&, int, const _Float16* const*, f4_t*) {}
+    template <int NB, int GS, bool SX> struct Tmp {};
+    template <int NB, int GS, bool SX>
+    TQ_DEV static void issue(const Raw&, int, const _Float16* const*, Tmp<NB, GS, SX>&) {}
+    template <int NB, int NV, int GS, bool SX>
+    TQ_DEV static void finish(const Tmp<NB, GS, SX>&, const Dec&, const float*, f4_t*) {}
     TQ_DEV static uint4 stage8(const _Float16* xr, int d0) { return FxNib<LAYOUT>::stage8(xr, d0); }
     TQ_DEV static int steps_per_group(const WDesc&) { return 1; }
 };
@@ -609,15 +639,13 @@ struct FxQ4K {
         }
         return j == 0 ? t + bias(d, s16) : t;
     }
-    template <int NB, int NV, int GS>
-    TQ_DEV static void fold_mfma(const Raw& r, const Dec& d, int j, const _Float16* const* xt,
-                                 f4_t* acc) {
+    template <int NB, int GS, bool SX>
+    struct Tmp { f4_t CA[2][NB], CB[2][NB], OA[SX ? 1 : 2][NB], OB[SX ? 1 : 2][NB]; };
+    template <int NB, int GS, bool SX>
+    TQ_DEV static void issue(const Raw& r, int j, const _Float16* const* xt, Tmp<NB, GS, SX>& T) {
         const h4_t ones = h4_of(kOnes2, kOnes2);
 #pragma unroll
         for (int h = 0; h < 2; h++) {  // the two 64-element groups of the chunk
-            f4_t CA[NB], CB[NB], OA[NB], OB[NB];
-#pragma unroll
-            for (int n = 0; n < NB; n++) { CA[n] = CB[n] = OA[n] = OB[n] = f4_zero(); }
 #pragma unroll
             for (int ii = 0; ii < 2; ii++) {
                 const int i = 2 * h + ii;
@@ -628,22 +656,39 @@ struct FxQ4K {
                 for (int n = 0; n < NB; n++) {
                     const uint4 xv = *(const uint4*)(xt[n] + 64 * h + 8 * (4 * ii + j));
                     const h4_t xa = h4_of(xv.x, xv.y), xb = h4_of(xv.z, xv.w);
-                    CA[n] = mfma16(xa, blo, CA[n]);
-                    CB[n] = mfma16(xb, bhi, CB[n]);
-                    OA[n] = mfma16(xa, ones, OA[n]);
-                    OB[n] = mfma16(xb, ones, OB[n]);
+                    T.CA[h][n] = mfma16(xa, blo, ii == 0 ? f4_zero() : T.CA[h][n]);
+                    T.CB[h][n] = mfma16(xb, bhi, ii == 0 ? f4_zero() : T.CB[h][n]);
+                    if constexpr (!SX) {
+                        T.OA[h][n] = mfma16(xa, ones, ii == 0 ? f4_zero() : T.OA[h][n]);
+                        T.OB[h][n] = mfma16(xb, ones, ii == 0 ? f4_zero() : T.OB[h][n]);
+                    }
                 }
             }
+        }
+    }
+    template <int NB, int NV, int GS, bool SX>
+    TQ_DEV static void finish(const Tmp<NB, GS, SX>& T, const Dec& d, const float* sx, f4_t* acc) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
             const float sa = d.ds[2 * h] * kTwo24, sb = d.ds[2 * h + 1] * (kTwo24 / 16.0f);
             const float ma = -d.dm[2 * h], mb = -d.dm[2 * h + 1];
+            float4 xa, xb;  // sub-block sums (32 columns each) for tokens 0..3
+            if constexpr (SX) {
+                xa = *(const float4*)(sx + 4 * (2 * h));
+                xb = *(const float4*)(sx + 4 * (2 * h + 1));
+            }
 #pragma unroll
             for (int n = 0; n < NB; n++)
 #pragma unroll
                 for (int v = 0; v < NV; v++) {
-                    float a = __builtin_fmaf(sa, CA[n][v], acc[n][v]);
-                    a = __builtin_fmaf(sb, CB[n][v], a);
-                    a = __builtin_fmaf(ma, OA[n][v], a);
-                    acc[n][v] = __builtin_fmaf(mb, OB[n][v], a);
+                    float t = __builtin_fmaf(sa, T.CA[h][n][v], acc[n][v]);
+                    t = __builtin_fmaf(sb, T.CB[h][n][v], t);
+                    const float oa = SX ? (v == 0 ? xa.x : v == 1 ? xa.y : v == 2 ? xa.z : xa.w)
+                                        : T.OA[SX ? 0 : h][n][v];
+                    const float ob = SX ? (v == 0 ? xb.x : v == 1 ? xb.y : v == 2 ? xb.z : xb.w)
+                                        : T.OB[SX ? 0 : h][n][v];
+                    t = __builtin_fmaf(ma, oa, t);
+                    acc[n][v] = __builtin_fmaf(mb, ob, t);
                 }
         }
     }
@@ -754,8 +799,11 @@ struct FxQ3K {
         t *= kTwo24;
         return j == 0 ? t + bias(d, s16) : t;
     }
-    template <int NB, int NV, int GS>
-    TQ_DEV static void fold_mfma(const Raw&, const Dec&, int, const _Float16* const*, f4_t*) {}
+    template <int NB, int GS, bool SX> struct Tmp {};
+    template <int NB, int GS, bool SX>
+    TQ_DEV static void issue(const Raw&, int, const _Float16* const*, Tmp<NB, GS, SX>&) {}
+    template <int NB, int NV, int GS, bool SX>
+    TQ_DEV static void finish(const Tmp<NB, GS, SX>&, const Dec&, const float*, f4_t*) {}
     TQ_DEV static uint4 stage8(const _Float16* xr, int d0) {
         // d0 = 16 * (8h + l4) + 8 * p: levels jj = 2p, 2p+1 of positions l..l+3
         const int e = d0 >> 4, h = e >> 3, l = (e & 7) * 4, jj = (d0 & 8) ? 2 : 0;
@@ -824,8 +872,11 @@ struct FxFp8 {
         }
         return (a + b) * 256.0f;
     }
-    template <int NB, int NV, int GS>
-    TQ_DEV static void fold_mfma(const Raw&, const Dec&, int, const _Float16* const*, f4_t*) {}
+    template <int NB, int GS, bool SX> struct Tmp {};
+    template <int NB, int GS, bool SX>
+    TQ_DEV static void issue(const Raw&, int, const _Float16* const*, Tmp<NB, GS, SX>&) {}
+    template <int NB, int NV, int GS, bool SX>
+    TQ_DEV static void finish(const Tmp<NB, GS, SX>&, const Dec&, const float*, f4_t*) {}
     TQ_DEV static uint4 stage8(const _Float16* xr, int d0) {
         _Float16 h[8], o[8];
         ldh8(xr + d0, h);

@@ -20,6 +20,9 @@
 
 namespace tq {
 
+#ifndef TQ_GEMV_U
+#define TQ_GEMV_U 4
+#endif
 constexpr int kGemvWaves = 4;
 constexpr int kGemvThreads = kGemvWaves * kWave;
 constexpr int kGemvLdsBytes = 32 * 1024;  // activation stage per workgroup
@@ -74,6 +77,33 @@ TQ_DEV void stage_f32(float* xf, float* s16, int pc, const void* x, int xdt, int
 
 // fp16 activations in the format's pairing order (F::stage8) and, for the
 // VALU fold, fp32 sums of every 16 columns.  Rows of x are 16-byte aligned.
+// SX (MFMA with at most 4 tokens): fp32 sums of every 32 columns for token
+// slots 0..3 at s16[4 * (col / 32) + token].
+template <int M>
+TQ_DEV void stage_sums32(float* sx, const void* x, int64_t ldx, int m0, int mcount, int col0,
+                         int ncols, int tid) {
+    for (int e = tid; e < 4 * (ncols >> 5); e += kGemvThreads) {
+        const int b = e >> 2, m = e & 3;
+        float s = 0.0f;
+        if (m < mcount && m < M) {
+            const _Float16* src = (const _Float16*)x + (int64_t)(m0 + m) * ldx + col0 + 32 * b;
+            float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 32; q += 8) {
+                _Float16 h[8];
+                ldh8(src + q, h);
+#pragma unroll
+                for (int i = 0; i < 8; i += 2) {
+                    a0 += (float)h[i];
+                    a1 += (float)h[i + 1];
+                }
+            }
+            s = a0 + a1;
+        }
+        sx[e] = s;
+    }
+}
+
 template <class F, int M, bool SUMS>
 TQ_DEV void stage_f16(_Float16* xh, float* s16, int pc, const void* x, int64_t ldx, int m0,
                       int mcount, int col0, int ncols, int tid) {
@@ -115,7 +145,8 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     const WDesc& W = P.w;
     const int rows = W.g.rows, nchunks = P.nchunks;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the wave index is uniform: keep the chunk bookkeeping in scalar registers
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int r = lane & 15, j = lane >> 4;
     // KS waves share one row tile and split its chunks (part, part + KS, ...)
     const int ks_log = P.ks_log, KS = 1 << ks_log;
@@ -125,13 +156,14 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
 
     float* xf = lds;
     _Float16* xh = (_Float16*)lds;
-    float* s16 = MODE == kModeF32 ? lds + M * pc : lds + M * pc / 2;
+    float* s16 = MODE == kModeF32 ? lds + M * pc : lds + M * pc / 2;  // MFMA + SX: 32-col sums
 
     const int row = tile * 16 + r;
     const typename F::Off off = F::base(W, row < rows ? row : rows - 1, j);  // past the end: not stored
 
     constexpr int NB = (M + 15) / 16;  // MFMA token blocks
     constexpr int NV = M < 4 ? M : 4;  // accumulator entries holding tokens
+    constexpr bool SX = MODE == kModeMfma && M <= 4;  // activation sums from LDS
     f4_t macc[NB];
     float acc[M];
 #pragma unroll
@@ -143,7 +175,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     // flight while the current group is folded.  Every wave runs the same
     // number of groups (chunks past the end are masked) so the staging
     // barriers line up.
-    constexpr int U = 4;
+    constexpr int U = TQ_GEMV_U;
     // chunks per phase: the LDS stage (pc columns) or the whole row, in
     // whole rounds of U chunks for each of the KS waves
     const int round = U << ks_log;
@@ -152,21 +184,19 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     const int nph = (nchunks + pchunks - 1) / pchunks;
     const int ngroups = nph * gpp;
 
-    // group q: phase q / gpp, chunks phase0 + ((q % gpp) * U + u) * KS + part
-    auto chunk_of = [&](int q, int u) {
-        const int ph = q / gpp;
-        return ph * pchunks + (((q - ph * gpp) * U + u) << ks_log) + part;
-    };
-    auto load_group = [&](int q, typename F::Raw (&R)[U]) {
+    // group q = ph * gpp + g: chunks ph * pchunks + (g * U + u) * KS + part.
+    // Groups are visited in order; the phase of a group is tracked
+    // incrementally (no division per chunk).
+    auto chunk_at = [&](int ph, int g, int u) { return ph * pchunks + ((g * U + u) << ks_log) + part; };
+    auto load_group = [&](int ph, int g, typename F::Raw (&R)[U]) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int cc = chunk_of(q, u);
+            const int cc = chunk_at(ph, g, u);
             F::template load<GS>(W, off, cc < nchunks ? cc : 0, j, R[u]);
         }
     };
-    auto fold_group = [&](int q, const typename F::Raw (&R)[U]) {
-        const int ph = q / gpp;
-        if (q == ph * gpp) {  // first group of a phase: stage its activations
+    auto fold_group = [&](int ph, int g, const typename F::Raw (&R)[U]) {
+        if (g == 0) {  // first group of a phase: stage its activations
             const int col0 = ph * pchunks * F::CHUNK_COLS;
             const int ncols = min(pchunks * F::CHUNK_COLS, W.g.cols - col0);
             __syncthreads();
@@ -174,25 +204,48 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
                 stage_f32<M>(xf, s16, pc, P.x, a.xdt, P.ldx, a.m0, a.mcount, col0, ncols, tid);
             else
                 stage_f16<F, M, MODE == kModeDot2>(xh, s16, pc, P.x, P.ldx, a.m0, a.mcount, col0, ncols, tid);
+            if constexpr (SX) stage_sums32<M>(s16, P.x, P.ldx, a.m0, a.mcount, col0, ncols, tid);
             __syncthreads();
         }
+        if constexpr (MODE == kModeMfma) {
+            // chunk u's MFMAs are issued before chunk u-1 is scaled
+            const _Float16* xt[NB];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int cc = chunk_of(q, u);
-            if (cc >= nchunks) continue;  // uniform per wave
-            const int lbase = (cc - ph * pchunks) * F::CHUNK_COLS;
-            const typename F::Dec dec = F::template decode<GS>(W, R[u], cc, j);
-            if constexpr (MODE == kModeMfma) {
+            for (int n = 0; n < NB; n++) {
                 // A-operand rows of padding tokens re-read token 0: they only
                 // feed accumulator rows that are never stored
-                const _Float16* xt[NB];
+                const int tok = 16 * n + r;
+                xt[n] = xh + (tok < M ? tok : 0) * pc;
+            }
+            typename F::template Tmp<NB, GS, SX> T[2];
 #pragma unroll
-                for (int n = 0; n < NB; n++) {
-                    const int tok = 16 * n + r;
-                    xt[n] = xh + (tok < M ? tok : 0) * pc + lbase;
+            for (int u = 0; u <= U; u++) {
+                if (u < U) {
+                    const int cc = chunk_at(ph, g, u);
+                    if (cc < nchunks) {
+                        const int lbase = (cc - ph * pchunks) * F::CHUNK_COLS;
+                        const _Float16* xu[NB];
+#pragma unroll
+                        for (int n = 0; n < NB; n++) xu[n] = xt[n] + lbase;
+                        F::template issue<NB, GS, SX>(R[u], j, xu, T[u & 1]);
+                    }
                 }
-                F::template fold_mfma<NB, NV, GS>(R[u], dec, j, xt, macc);
-            } else {
+                if (u > 0) {
+                    const int cp = chunk_at(ph, g, u - 1);
+                    if (cp < nchunks) {
+                        const int lbase = (cp - ph * pchunks) * F::CHUNK_COLS;
+                        const typename F::Dec dec = F::template decode<GS>(W, R[u - 1], cp, j);
+                        F::template finish<NB, NV, GS, SX>(T[(u - 1) & 1], dec, s16 + 4 * (lbase >> 5), macc);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int cc = chunk_at(ph, g, u);
+                if (cc >= nchunks) continue;  // uniform per wave
+                const int lbase = (cc - ph * pchunks) * F::CHUNK_COLS;
+                const typename F::Dec dec = F::template decode<GS>(W, R[u], cc, j);
 #pragma unroll
                 for (int m = 0; m < M; m++) {
                     if constexpr (MODE == kModeF32)
@@ -207,13 +260,24 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     };
 
     typename F::Raw ra[U], rb[U];
-    load_group(0, ra);
-    for (int q = 0; q < ngroups; q += 2) {
-        if (q + 1 < ngroups) load_group(q + 1, rb);
-        fold_group(q, ra);
-        if (q + 1 >= ngroups) break;
-        if (q + 2 < ngroups) load_group(q + 2, ra);
-        fold_group(q + 1, rb);
+    // (ph, g) of the group being folded; the next group's loads go out first
+    int ph = 0, g = 0;
+    auto advance = [&](int& p, int& q) {
+        if (++q == gpp) { q = 0; ++p; }
+    };
+    load_group(0, 0, ra);
+    for (int n = 0; n < ngroups; n += 2) {
+        int ph1 = ph, g1 = g;
+        advance(ph1, g1);
+        if (n + 1 < ngroups) load_group(ph1, g1, rb);
+        fold_group(ph, g, ra);
+        if (n + 1 >= ngroups) break;
+        int ph2 = ph1, g2 = g1;
+        advance(ph2, g2);
+        if (n + 2 < ngroups) load_group(ph2, g2, ra);
+        fold_group(ph1, g1, rb);
+        ph = ph2;
+        g = g2;
     }
 
     // per-lane results: MFMA lane (r, q = j) holds tokens 16n + 4j + v of row
@@ -346,7 +410,7 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
     if (cap < step) cap = step;
     const int need = (maxcols + step - 1) / step * step;
     a.pc = need < cap ? need : cap;
-    const size_t stage = (size_t)M * a.pc * per4 / 4 + 16;
+    const size_t stage = (size_t)M * a.pc * per4 / 4 + (MODE == kModeMfma ? a.pc / 2 : 0) + 16;
     const size_t red = (size_t)kGemvWaves * M * 16 * 4;
     const size_t lds = stage > red ? stage : red;
     // workgroups: long-K problems first (they take longest)
