@@ -126,7 +126,8 @@ def bench_int4_layer(M, steps, warmup, gen):
     Xs = [X[m["cols"]] for m in layer]
     Ys = [torch.empty(M, m["rows"], device="cuda", dtype=torch.float16) for m in layer]
     abytes = sum(M * m["cols"] * 2 + M * m["rows"] * 2 for m in layer)
-    ms = time_launches(lambda i: tq.qgemm_batched(Ws[i % R], Xs, Ys), steps, warmup)
+    calls = [tq.PreparedBatch(w, Xs, Ys) for w in Ws]
+    ms = time_launches(lambda i: calls[i % R](), steps, warmup)
     total = wbytes + abytes
     return dict(ms=ms, bytes=total, wbytes=wbytes, gbs=total / ms / 1e6, copies=R,
                 layer=layer, flops=2 * M * sum(m["rows"] * m["cols"] for m in layer))
@@ -250,6 +251,36 @@ def cpu_model():
     return platform.processor()
 
 
+# ---------------------------------------------------------------- HBM traffic
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qgemv_int4_llama8b_m1_traffic.md")
+COPY_CALIB_BYTES = 1 << 30
+
+
+def copy_calibration():
+    """A plain device copy of COPY_CALIB_BYTES: its FETCH_SIZE / WRITE_SIZE per
+    dispatch is the scale that turns those counters into HBM bytes."""
+    import torch
+    src = torch.empty(COPY_CALIB_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copied {COPY_CALIB_BYTES} bytes 5 times")
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the headline kernel, from the committed
+    rocprofv3 --pmc summary: the line `traffic_bytes_per_launch: <n>`."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 # ---------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser()
@@ -258,6 +289,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only run a plain 1 GiB device copy (HBM byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -265,6 +298,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calib:
+        copy_calibration()
+        return
     import titan_qmm as tq
     tq.lib()
     gen = torch.Generator(device="cuda").manual_seed(0)
@@ -322,15 +358,19 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4 codes, fp16 scale/bias, fp16 x, fp32 accumulate",
+        "dtype": "int4",
         "data": "synthetic: weights N(0,0.02) quantized on the GPU with the convert_titan.py "
                 "INT4 recipe; x ~ N(0,1) fp16",
         "config": {"workload": "INT4 g128 dequant-GEMV, one Llama-3-8B layer (q,k,v,o,gate,up,down), "
                                "M=1, tiled layout, one batched launch per step",
+                   "arithmetic": "int4 codes x fp16 activations, fp32 accumulate, fp16 out",
                    "algorithmic_bytes_per_step": h["bytes"], "weight_bytes": h["wbytes"],
                    "weight_copies_rotated": h["copies"]},
         "roofline": {"bound": "hbm", "achieved": round(h["gbs"], 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(h["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(h["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profile(), "kernel": "qgemv_kernel (INT4 tiled, MFMA fold)",
+                     "algorithmic_bytes_per_launch": h["bytes"],
+                     "timing": "torch.cuda.Event pair on the launch stream around all timed launches"},
         "cpu_baseline": cpu,
         "cpu_baseline_all_cores": cpu_mt,
         "secondary": secondary,

@@ -199,6 +199,26 @@ def qgemm_batched(Ws, Xs, Ys, stream=None):
            "titan_qgemm_batched")
 
 
+class PreparedBatch:
+    """qgemm_batched with its C arguments built once: calling it issues one
+    titan_qgemm_batched on the stream given at preparation (for replaying the
+    same weights/activations/outputs in a decode loop)."""
+
+    def __init__(self, Ws, Xs, Ys, stream=None):
+        n = len(Ws)
+        self._keep = (Ws, Xs, Ys)
+        self._args = ((QWeightC * n)(*[w.cstruct() for w in Ws]),
+                      (_P * n)(*[_ptr(x) for x in Xs]), (_P * n)(*[_ptr(y) for y in Ys]), n,
+                      dtype_code(Xs[0].dtype), dtype_code(Ys[0].dtype),
+                      Xs[0].shape[0] if Xs[0].dim() == 2 else 1, _stream(stream))
+        self._fn = lib().titan_qgemm_batched
+
+    def __call__(self):
+        st = self._fn(*self._args)
+        if st:
+            _check(st, "titan_qgemm_batched")
+
+
 def qdequant(W, out_dtype=None, stream=None):
     import torch
     out = torch.empty((W.rows, W.cols), dtype=out_dtype or torch.float32, device="cuda")
