@@ -168,6 +168,43 @@ int titan_fused_moe_combine_norm(float* output, float* residual, const float* ex
                                  float shared_weight, const float* norm_weight, int dim,
                                  int num_active, float eps, hipStream_t stream);
 
+/* ======================================================================== */
+/* NVFP4 MoE grouped-expert forward (moe.cpp:874-1005 expert loop, with the */
+/* fp4.cu:187-252 dequant, activation.cu:17-32 SwiGLU and                   */
+/* activation.cu:111-139 combine), all tokens in four launches.             */
+/* ======================================================================== */
+/* One expert: three NVFP4 matrices in TITAN_LAYOUT_TILED (titan_repack_host
+ * of the reference's U8 codes + E4M3 block-16 scales), gate/up [inter][hidden],
+ * down [hidden][inter], each with its fp32 global scale. */
+typedef struct titan_nvfp4_expert {
+    const void* gate;
+    const void* up;
+    const void* down;
+    float gate_scale;
+    float up_scale;
+    float down_scale;
+} titan_nvfp4_expert;
+
+/* Device workspace for titan_moe_nvfp4_forward (bytes, 256-aligned base). */
+size_t titan_moe_nvfp4_workspace_bytes(int tokens, int k, int num_experts, int hidden,
+                                       int inter);
+
+/* out[t] = residual[t] + sum_j weights[t][j] * E_{indices[t][j]}(x[t])
+ *          (+ shared_weight * shared[t]),
+ * E(x) = Wd (silu(Wg x) * (Wu x)).  `experts` is a DEVICE array of
+ * num_experts descriptors; x [tokens][hidden] fp32/fp16/bf16; indices /
+ * weights [tokens][k] (e.g. from titan_moe_topk_batched); residual and shared
+ * [tokens][hidden] fp32 or NULL; out [tokens][hidden] in out_dtype.  The
+ * activations enter the matrix cores as fp16; the SwiGLU output is kept as
+ * fp16; accumulation and the combine are fp32.  hidden and inter must be
+ * multiples of 512. */
+int titan_moe_nvfp4_forward(const titan_nvfp4_expert* experts, int num_experts, int hidden,
+                            int inter, const void* x, int x_dtype, int tokens,
+                            const int* indices, const float* weights, int k,
+                            const float* residual, const float* shared, float shared_weight,
+                            void* out, int out_dtype, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream);
+
 /* ---- library info -------------------------------------------------------- */
 const char* titan_version(void);
 const char* titan_status_string(int status);

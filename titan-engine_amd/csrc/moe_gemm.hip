@@ -1,0 +1,439 @@
+// moe_gemm.hip -- NVFP4 grouped-expert MoE forward on gfx950.
+//
+// Restates the reference's expert loop (moe.cpp:874-1005): for every token and
+// each of its k selected experts, g = Wg x and u = Wu x with the NVFP4 dequant
+// of fp4.cu:187-252, a = silu(g) * u (activation.cu:17-32), y = Wd a, then the
+// weighted combine into the residual (activation.cu:111-139).  Instead of
+// 3 GEMV launches per (token, expert) it runs four launches for all tokens:
+//
+//   1. permute   group the (token, slot) pairs by expert (counting sort)
+//   2. gate/up   per (expert, 64-row block): both projections of all of the
+//                expert's tokens in one pass over the weights, SwiGLU fused,
+//                activations written as fp16 rows in expert order
+//   3. down      per (expert, 64-row block), fp32 rows in expert order
+//   4. combine   per token: residual + sum_j w_j y_j (+ shared), in slot order
+//
+// GEMM kernel: one wave owns a 16-row tile of the weights (TILED NVFP4 layout)
+// and runs v_mfma_f32_16x16x32_f16 with the tokens as A (staged per K-slab in
+// LDS as fp16) and the weights as B.  A lane's code word holds 8 consecutive
+// columns of one 16-column scale block, so its B operand is
+//   cvt_scalef32_pk_f16_fp4(word, 2^8) * (e4m3 scale as fp16 * 2^-8)
+// -- four conversions and four packed multiplies per 8 weights, all exact
+// (E2M1 x E4M3 products have at most 5 significant bits and stay inside the
+// fp16 normal range); the fp32 global scale multiplies the accumulator.
+#include "common.h"
+#include "layout.h"
+
+namespace tq {
+
+typedef _Float16 mh8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mh2 __attribute__((ext_vector_type(2)));
+typedef float mf4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMoeThreads = 256;
+constexpr int kMoeRowsPerWg = 64;  // 4 waves x 16 rows
+constexpr int kMoeMaxExperts = 4096;
+
+struct MoeGemmArgs {
+    const titan_nvfp4_expert* experts;  // device array [E]
+    const void* x;                      // activation rows
+    int64_t ldx;                        // elements between activation rows
+    const int* pair_at;                 // gate/up: position -> pair id; down: nullptr
+    int k;                              // experts per token (pair id / k = token)
+    const int* off;                     // [E + 1] first position of each expert
+    int N, K;                           // weight rows / columns
+    void* out;                          // gate/up: fp16 [P][N]; down: fp32 [P][N]
+    int64_t ldo;
+};
+
+// e4m3 byte (fp4.cu:173-185 semantics: 0x7F / 0xFF -> 0) as fp16 bits of
+// value * 2^-8: the exponent fields differ by 8 in bias, so it is a shift.
+TQ_DEV uint32_t e4m3_h16_scaled(uint32_t b) {
+    const uint32_t m = b & 0x7Fu;
+    const uint32_t h = ((b & 0x80u) << 8) | (m << 7);
+    return m == 0x7Fu ? 0u : h;
+}
+
+// 8 fp4 codes of one word (low nibble first) times one scale -> B operand.
+TQ_DEV mh8 nvfp4_b8(uint32_t w, uint32_t sc16) {
+    const mh2 s = __builtin_bit_cast(mh2, sc16 | (sc16 << 16));
+    const mh2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 256.0f, 0) * s;
+    const mh2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 256.0f, 1) * s;
+    const mh2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 256.0f, 2) * s;
+    const mh2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 256.0f, 3) * s;
+    return mh8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// 8 activation elements of one source dtype, converted to fp16 for LDS.
+template <int XDT>
+struct XItem;
+template <>
+struct XItem<TITAN_FP16> {
+    uint4 a;
+    TQ_DEV void load(const void* p, int64_t e) { a = *(const uint4*)((const uint16_t*)p + e); }
+    TQ_DEV void zero() { a = make_uint4(0, 0, 0, 0); }
+    TQ_DEV uint4 h() const { return a; }
+};
+template <>
+struct XItem<TITAN_BF16> {
+    uint4 a;
+    TQ_DEV void load(const void* p, int64_t e) { a = *(const uint4*)((const uint16_t*)p + e); }
+    TQ_DEV void zero() { a = make_uint4(0, 0, 0, 0); }
+    TQ_DEV static uint32_t cv(uint32_t w) {
+        const mh2 v = {(_Float16)bf16_to_f32(w & 0xFFFFu), (_Float16)bf16_to_f32(w >> 16)};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+    TQ_DEV uint4 h() const { return make_uint4(cv(a.x), cv(a.y), cv(a.z), cv(a.w)); }
+};
+template <>
+struct XItem<TITAN_FP32> {
+    float4 a, b;
+    TQ_DEV void load(const void* p, int64_t e) {
+        a = *(const float4*)((const float*)p + e);
+        b = *(const float4*)((const float*)p + e + 4);
+    }
+    TQ_DEV void zero() { a = b = make_float4(0, 0, 0, 0); }
+    TQ_DEV static uint32_t cv(float x, float y) {
+        const mh2 v = {(_Float16)x, (_Float16)y};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+    TQ_DEV uint4 h() const { return make_uint4(cv(a.x, a.y), cv(a.z, a.w), cv(b.x, b.y), cv(b.z, b.w)); }
+};
+
+// TM tokens per pass, SL columns per LDS slab (TM * SL = 8192 elements, so
+// every thread stages 4 items of 8 elements per slab).  GATED: gate and up
+// together with the SwiGLU epilogue; otherwise one matrix, fp32 rows out.
+template <int TM, int SL, bool GATED, int XDT>
+__global__ __launch_bounds__(kMoeThreads) void moe_gemm_kernel(MoeGemmArgs a) {
+    constexpr int NB = TM / 16;         // MFMA token blocks
+    constexpr int CPS = SL / 128;       // 64-byte chunks per slab
+    constexpr int LDR = SL + 8;         // halves per LDS row (16 B pad)
+    constexpr int NI = TM * SL / 8 / kMoeThreads;
+    constexpr int NM = GATED ? 2 : 1;
+    static_assert(NI == 4, "staging geometry");
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][TM * LDR];
+
+    const int e = blockIdx.y;
+    const int beg = a.off[e], n_e = a.off[e + 1] - beg;
+    if (n_e <= 0) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane >> 4, r = lane & 15;
+    const int row0 = blockIdx.x * kMoeRowsPerWg + wave * 16;
+    const titan_nvfp4_expert ex = a.experts[e];
+    const uint8_t* W[2] = {(const uint8_t*)(GATED ? ex.gate : ex.down), (const uint8_t*)ex.up};
+    const float gsc[2] = {GATED ? ex.gate_scale : ex.down_scale, ex.up_scale};
+    const Geo geo = make_geo(TITAN_NVFP4, a.N, a.K, 16);
+    const uint32_t code_off = (uint32_t)tiled_code_off(geo, row0 + r, 0, j);
+    const uint32_t sc_off = (uint32_t)tiled_nvs_off(geo, row0 + r, 0);
+    const int nslab = a.K / SL;
+    const int sh = 8 * (j >> 1);  // byte of the lane's scale within a half chunk
+
+    for (int t0 = 0; t0 < n_e; t0 += TM) {
+        const int nt = min(TM, n_e - t0), nb = (nt + 15) >> 4;
+        // staging sources: item it covers row rr, columns [8 cg, 8 cg + 8) of the slab
+        int64_t src[NI];
+        int ldsi[NI];
+#pragma unroll
+        for (int it = 0; it < NI; it++) {
+            const int idx = it * kMoeThreads + tid, rr = idx / (SL / 8), cg = idx % (SL / 8);
+            ldsi[it] = rr * LDR + cg * 8;
+            int64_t srow = -1;
+            if (rr < nt) srow = a.pair_at ? a.pair_at[beg + t0 + rr] / a.k : beg + t0 + rr;
+            src[it] = srow < 0 ? -1 : srow * a.ldx + cg * 8;
+        }
+        auto load_x = [&](int s, XItem<XDT>* xr) {
+#pragma unroll
+            for (int it = 0; it < NI; it++) {
+                if (src[it] >= 0) xr[it].load(a.x, src[it] + (int64_t)s * SL);
+                else xr[it].zero();
+            }
+        };
+        struct WSet { uint4 c[NM][CPS]; uint2 s[NM][CPS]; };
+        auto load_w = [&](int s, WSet& w) {
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int c = 0; c < CPS; c++) {
+                    const uint32_t ch = (uint32_t)(s * CPS + c);
+                    w.c[m][c] = *(const uint4*)(W[m] + code_off + ch * 1024u);
+                    w.s[m][c] = *(const uint2*)(W[m] + sc_off + ch * 128u);
+                }
+        };
+
+        mf4 acc[NM][NB];
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int b = 0; b < NB; b++) acc[m][b] = mf4{0, 0, 0, 0};
+
+        XItem<XDT> xr[NI];
+        WSet wc, wn;
+        load_w(0, wc);
+        load_x(0, xr);
+        for (int s = 0; s < nslab; s++) {
+            _Float16* buf = xs[s & 1];
+#pragma unroll
+            for (int it = 0; it < NI; it++) *(uint4*)(buf + ldsi[it]) = xr[it].h();
+            if (s + 1 < nslab) {
+                load_w(s + 1, wn);
+                load_x(s + 1, xr);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int c = 0; c < CPS; c++) {
+                uint32_t scw[NM][4];
+#pragma unroll
+                for (int m = 0; m < NM; m++) {
+                    scw[m][0] = e4m3_h16_scaled((wc.s[m][c].x >> sh) & 0xFFu);
+                    scw[m][1] = e4m3_h16_scaled((wc.s[m][c].x >> (16 + sh)) & 0xFFu);
+                    scw[m][2] = e4m3_h16_scaled((wc.s[m][c].y >> sh) & 0xFFu);
+                    scw[m][3] = e4m3_h16_scaled((wc.s[m][c].y >> (16 + sh)) & 0xFFu);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    mh8 B[NM];
+#pragma unroll
+                    for (int m = 0; m < NM; m++) {
+                        const uint4 cw = wc.c[m][c];
+                        const uint32_t w = i == 0 ? cw.x : i == 1 ? cw.y : i == 2 ? cw.z : cw.w;
+                        B[m] = nvfp4_b8(w, scw[m][i]);
+                    }
+#pragma unroll
+                    for (int b = 0; b < NB; b++) {
+                        if (b < nb) {
+                            const mh8 A = *(const mh8*)(buf + (b * 16 + r) * LDR + c * 128 + 32 * i + 8 * j);
+#pragma unroll
+                            for (int m = 0; m < NM; m++)
+                                acc[m][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[m], acc[m][b], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+            wc = wn;
+        }
+
+        // epilogue: lane holds weight row row0 + r for tokens 16 b + 4 j + v
+        const int row = row0 + r;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            if (b >= nb) break;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int tok = b * 16 + 4 * j + v;
+                if (tok >= nt) continue;
+                const int64_t o = (int64_t)(beg + t0 + tok) * a.ldo + row;
+                if constexpr (GATED) {
+                    const float g = acc[0][b][v] * gsc[0], u = acc[1][b][v] * gsc[1];
+                    const float act = (g * (1.0f / (1.0f + expf(-g)))) * u;
+                    ((_Float16*)a.out)[o] = (_Float16)act;
+                } else {
+                    ((float*)a.out)[o] = acc[0][b][v] * gsc[0];
+                }
+            }
+        }
+        __syncthreads();  // the next token pass rewrites both LDS buffers
+    }
+}
+
+// Counting sort of the (token, slot) pairs by expert.  One workgroup; the
+// order of pairs inside an expert is irrelevant to the results (each token is
+// its own row of the GEMMs and the combine reads positions through `inv`).
+__global__ __launch_bounds__(1024) void moe_permute_kernel(const int* __restrict__ idx, int P,
+                                                           int E, int* __restrict__ off,
+                                                           int* __restrict__ pair_at,
+                                                           int* __restrict__ inv) {
+    __shared__ int cnt[kMoeMaxExperts];
+    __shared__ int part[1024];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+    __syncthreads();
+    for (int p = tid; p < P; p += 1024) {
+        const int e = idx[p];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    // exclusive scan: thread t owns experts [4t, 4t + 4)
+    int loc[4], s = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int e = 4 * tid + q;
+        loc[q] = s;
+        s += e < E ? cnt[e] : 0;
+    }
+    part[tid] = s;
+    __syncthreads();
+    for (int d = 1; d < 1024; d <<= 1) {
+        const int v = tid >= d ? part[tid - d] : 0;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    const int base = part[tid] - s;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int e = 4 * tid + q;
+        if (e < E) {
+            off[e] = base + loc[q];
+            cnt[e] = base + loc[q];
+        }
+    }
+    if (tid == 1023) off[E] = part[1023];
+    __syncthreads();
+    for (int p = tid; p < P; p += 1024) {
+        const int e = idx[p];
+        if (e >= 0 && e < E) {
+            const int pos = atomicAdd(&cnt[e], 1);
+            pair_at[pos] = p;
+            inv[p] = pos;
+        } else {
+            inv[p] = -1;
+        }
+    }
+}
+
+// activation.cu:111-139 per token: c = sum_j y_j * w_j (fused multiply-add in
+// slot order), + shared * w_s, out = residual + c.
+__global__ __launch_bounds__(256) void moe_combine_rows_kernel(
+    const float* __restrict__ y, const int* __restrict__ inv, const float* __restrict__ w,
+    int k, int dim, const float* __restrict__ residual, const float* __restrict__ shared,
+    float sw, void* __restrict__ out, int out_dtype) {
+    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= dim) return;
+    float c = 0.0f;
+    for (int q = 0; q < k; q++) {
+        const int pos = inv[(int64_t)t * k + q];
+        if (pos >= 0) c = __builtin_fmaf(y[(int64_t)pos * dim + i], w[(int64_t)t * k + q], c);
+    }
+    if (shared) c = __builtin_fmaf(shared[(int64_t)t * dim + i], sw, c);
+    const float v = (residual ? residual[(int64_t)t * dim + i] : 0.0f) + c;
+    store_out(out, (int64_t)t * dim + i, out_dtype, v);
+}
+
+}  // namespace tq
+
+namespace {
+
+using namespace tq;
+
+struct MoeWs {
+    int* off;
+    int* pair_at;
+    int* inv;
+    _Float16* act;
+    float* y;
+    size_t bytes;
+};
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+MoeWs carve(void* base, int tokens, int k, int E, int hidden, int inter) {
+    const size_t P = (size_t)tokens * k;
+    MoeWs w;
+    size_t o = 0;
+    auto take = [&](size_t n) { size_t at = o; o = align256(o + n); return at; };
+    const size_t o_off = take((size_t)(E + 1) * 4), o_pair = take(P * 4), o_inv = take(P * 4),
+                 o_act = take(P * inter * 2), o_y = take(P * hidden * 4);
+    char* b = (char*)base;
+    w.off = (int*)(b + o_off);
+    w.pair_at = (int*)(b + o_pair);
+    w.inv = (int*)(b + o_inv);
+    w.act = (_Float16*)(b + o_act);
+    w.y = (float*)(b + o_y);
+    w.bytes = o;
+    return w;
+}
+
+template <int TM, int SL, bool GATED>
+int launch_moe(const MoeGemmArgs& a, int x_dtype, int E, hipStream_t st) {
+    dim3 grid(a.N / kMoeRowsPerWg, E);
+    switch (x_dtype) {
+        case TITAN_FP16:
+            hipLaunchKernelGGL((moe_gemm_kernel<TM, SL, GATED, TITAN_FP16>), grid, dim3(kMoeThreads), 0, st, a);
+            break;
+        case TITAN_BF16:
+            hipLaunchKernelGGL((moe_gemm_kernel<TM, SL, GATED, TITAN_BF16>), grid, dim3(kMoeThreads), 0, st, a);
+            break;
+        default:
+            hipLaunchKernelGGL((moe_gemm_kernel<TM, SL, GATED, TITAN_FP32>), grid, dim3(kMoeThreads), 0, st, a);
+            break;
+    }
+    return tqh::launch_status();
+}
+
+template <bool GATED>
+int launch_moe_tm(int tm, const MoeGemmArgs& a, int x_dtype, int E, hipStream_t st) {
+    if (tm == 16) return launch_moe<16, 512, GATED>(a, x_dtype, E, st);
+    if (tm == 32) return launch_moe<32, 256, GATED>(a, x_dtype, E, st);
+    return launch_moe<64, 128, GATED>(a, x_dtype, E, st);
+}
+
+}  // namespace
+
+extern "C" size_t titan_moe_nvfp4_workspace_bytes(int tokens, int k, int num_experts, int hidden,
+                                                 int inter) {
+    if (tokens <= 0 || k <= 0 || num_experts <= 0 || hidden <= 0 || inter <= 0) return 0;
+    return carve(nullptr, tokens, k, num_experts, hidden, inter).bytes;
+}
+
+extern "C" int titan_moe_nvfp4_forward(const titan_nvfp4_expert* experts, int num_experts,
+                                       int hidden, int inter, const void* x, int x_dtype,
+                                       int tokens, const int* indices, const float* weights,
+                                       int k, const float* residual, const float* shared,
+                                       float shared_weight, void* out, int out_dtype,
+                                       void* workspace, size_t workspace_bytes,
+                                       hipStream_t stream) {
+    if (!experts || !x || !indices || !weights || !out || !workspace) return TITAN_ERR_INVALID_ARG;
+    if (tokens <= 0 || k <= 0 || num_experts <= 0 || num_experts > kMoeMaxExperts)
+        return TITAN_ERR_INVALID_ARG;
+    if (!tqh::act_dtype_ok(x_dtype) || !tqh::act_dtype_ok(out_dtype)) return TITAN_ERR_INVALID_ARG;
+    // shapes: 64-row blocks of both projections, 512-column K slabs, tileable NVFP4
+    if (hidden % 512 || inter % 512) return TITAN_ERR_UNSUPPORTED;
+    if ((int64_t)tokens * k > (1 << 30)) return TITAN_ERR_UNSUPPORTED;
+    if (!tq::tiled_total_bytes(TITAN_NVFP4, inter, hidden, 16) ||
+        !tq::tiled_total_bytes(TITAN_NVFP4, hidden, inter, 16))
+        return TITAN_ERR_UNSUPPORTED;
+    if (((uintptr_t)x & 15) || ((uintptr_t)workspace & 255)) return TITAN_ERR_INVALID_ARG;
+    const MoeWs ws = carve(workspace, tokens, k, num_experts, hidden, inter);
+    if (workspace_bytes < ws.bytes) return TITAN_ERR_WORKSPACE;
+
+    const int P = tokens * k;
+    hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), 0, stream, indices, P,
+                       num_experts, ws.off, ws.pair_at, ws.inv);
+    if (int st = tqh::launch_status()) return st;
+
+    // tokens per pass from the mean load per expert
+    const int avg = (P + num_experts - 1) / num_experts;
+    const int tm = avg <= 8 ? 16 : avg <= 24 ? 32 : 64;
+
+    MoeGemmArgs g{};
+    g.experts = experts;
+    g.x = x;
+    g.ldx = hidden;
+    g.pair_at = ws.pair_at;
+    g.k = k;
+    g.off = ws.off;
+    g.N = inter;
+    g.K = hidden;
+    g.out = ws.act;
+    g.ldo = inter;
+    if (int st = launch_moe_tm<true>(tm, g, x_dtype, num_experts, stream)) return st;
+
+    MoeGemmArgs d{};
+    d.experts = experts;
+    d.x = ws.act;
+    d.ldx = inter;
+    d.pair_at = nullptr;
+    d.k = k;
+    d.off = ws.off;
+    d.N = hidden;
+    d.K = inter;
+    d.out = ws.y;
+    d.ldo = hidden;
+    if (int st = launch_moe_tm<false>(tm, d, TITAN_FP16, num_experts, stream)) return st;
+
+    hipLaunchKernelGGL(moe_combine_rows_kernel, dim3((hidden + 255) / 256, tokens), dim3(256), 0,
+                       stream, ws.y, ws.inv, weights, k, hidden, residual, shared, shared_weight,
+                       out, out_dtype);
+    return tqh::launch_status();
+}

@@ -62,6 +62,9 @@ _SIGS = {
     "titan_moe_topk_batched": [_P, _P, _P, _I, _I, _I, _P],
     "titan_swiglu": [_P, _P, _P, _I, _P],
     "titan_fused_moe_combine_norm": [_P, _P, _P, _P, _P, _F, _P, _I, _I, _F, _P],
+    "titan_moe_nvfp4_workspace_bytes": [_I, _I, _I, _I, _I],
+    "titan_moe_nvfp4_forward": [_P, _I, _I, _I, _P, _I, _I, _P, _P, _I, _P, _P, _F, _P, _I,
+                                _P, _SZ, _P],
     "titan_version": [],
     "titan_status_string": [_I],
 }
@@ -79,6 +82,7 @@ def lib():
             fn.argtypes = args
             fn.restype = _I
         L.titan_tiled_bytes.restype = _SZ
+        L.titan_moe_nvfp4_workspace_bytes.restype = _SZ
         L.titan_version.restype = ctypes.c_char_p
         L.titan_status_string.restype = ctypes.c_char_p
         _LIB = L
@@ -294,3 +298,35 @@ def fused_moe_combine_norm(out, residual, expert_out, w, shared, shared_w, dim, 
                                               _ptr(w), _ptr(shared), float(shared_w), None, dim,
                                               na, 1e-5, _stream(stream)),
            "fused_moe_combine_norm")
+
+
+class NvExpertC(ctypes.Structure):
+    """titan_nvfp4_expert: device pointers to the three TILED NVFP4 matrices
+    and their fp32 global scales."""
+    _fields_ = [("gate", _P), ("up", _P), ("down", _P), ("gate_scale", ctypes.c_float),
+                ("up_scale", ctypes.c_float), ("down_scale", ctypes.c_float)]
+
+
+def nvfp4_expert_table(experts):
+    """[(gate_dev, up_dev, down_dev, gs_gate, gs_up, gs_down)] -> device uint8
+    tensor holding the titan_nvfp4_expert array (keep the weight tensors alive)."""
+    import torch
+    arr = (NvExpertC * len(experts))(*[NvExpertC(_ptr(g), _ptr(u), _ptr(d), float(a), float(b),
+                                                 float(c)) for g, u, d, a, b, c in experts])
+    host = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
+    return host.cuda()
+
+
+def moe_nvfp4_workspace_bytes(tokens, k, E, hidden, inter):
+    return int(lib().titan_moe_nvfp4_workspace_bytes(tokens, k, E, hidden, inter))
+
+
+def moe_nvfp4_forward(table, E, hidden, inter, x, indices, weights, out, workspace,
+                      residual=None, shared=None, shared_weight=0.0, stream=None):
+    T, k = indices.shape
+    _check(lib().titan_moe_nvfp4_forward(_ptr(table), E, hidden, inter, _ptr(x),
+                                         dtype_code(x.dtype), T, _ptr(indices), _ptr(weights), k,
+                                         _ptr(residual), _ptr(shared), float(shared_weight),
+                                         _ptr(out), dtype_code(out.dtype), _ptr(workspace),
+                                         workspace.numel() * workspace.element_size(),
+                                         _stream(stream)), "moe_nvfp4_forward")
