@@ -192,6 +192,61 @@ def bench_fp8(M, N, K, gen, steps, warmup):
     return dict(ms=ms, tflops=fl / ms / 1e9, gemm_ms=gemm_ms, gemm_tflops=fl / gemm_ms / 1e9)
 
 
+NV_EXPERT_BYTES = 3 * (2048 * 7168 // 2 + 2048 * 7168 // 16 + 4)  # codes + e4m3 + global
+
+
+def make_nvfp4_experts(E, hidden, inter, gen):
+    """Synthetic NVFP4 experts directly in the TILED layout: uniform random
+    E2M1 codes and E4M3 block scales in [2^-3, 2^2] (no NaN code), fp32
+    global scales; the repack is a byte permutation, so random bytes in the
+    tiled layout are a valid repacked tensor."""
+    import torch
+    import titan_qmm as tq
+    mats = []
+    for _ in range(E):
+        trip = []
+        for n, k in ((inter, hidden), (inter, hidden), (hidden, inter)):
+            nb = tq.tiled_bytes(tq.NVFP4, n, k)
+            t = torch.randint(0, 256, (nb,), generator=gen, device="cuda", dtype=torch.int32)
+            t = t.to(torch.uint8)
+            code_bytes = n * k // 2
+            t[code_bytes:] = torch.randint(0x28, 0x48, (nb - code_bytes,), generator=gen,
+                                           device="cuda", dtype=torch.int32).to(torch.uint8)
+            trip.append(t)
+        mats.append(trip)
+    table = tq.nvfp4_expert_table([(g, u, d, 0.02 / 448, 0.02 / 448, 0.02 / 448)
+                                   for g, u, d in mats])
+    return mats, table
+
+
+def bench_moe(T, steps, warmup, gen, experts=None):
+    """C4: DeepSeek-V3-like NVFP4 MoE layer, 256 experts, top-8, hidden 7168,
+    inter 2048, T tokens; one step = GPU top-k routing of N(0,1) logits + the
+    grouped-expert forward (permute, gate/up+SwiGLU, down, combine)."""
+    import torch
+    import titan_qmm as tq
+    E, hidden, inter, k = 256, 7168, 2048, 8
+    mats, table = experts if experts is not None else make_nvfp4_experts(E, hidden, inter, gen)
+    logits = torch.randn(T, E, generator=gen, device="cuda")
+    x = torch.randn(T, hidden, generator=gen, device="cuda").to(torch.bfloat16)
+    w = torch.empty(T, k, device="cuda")
+    idx = torch.empty(T, k, dtype=torch.int32, device="cuda")
+    out = torch.empty(T, hidden, device="cuda", dtype=torch.bfloat16)
+    ws = torch.empty(tq.moe_nvfp4_workspace_bytes(T, k, E, hidden, inter), dtype=torch.uint8,
+                     device="cuda")
+
+    def step(i):
+        tq.moe_topk_batched(logits, w, idx, k)
+        tq.moe_nvfp4_forward(table, E, hidden, inter, x, idx, w, out, ws)
+
+    ms = time_launches(step, steps, warmup)
+    used = int(torch.unique(idx).numel())
+    nbytes = used * NV_EXPERT_BYTES + T * hidden * 2 * 2 + T * E * 4
+    flops = 2.0 * T * k * 3 * inter * hidden
+    return dict(ms=ms, experts_hit=used, bytes=nbytes, gbs=nbytes / ms / 1e6,
+                tflops=flops / ms / 1e9), (mats, table)
+
+
 # ---------------------------------------------------------------- CPU baseline
 def cpu_baseline(layer, budget_s=12.0):
     """The reference's own AVX-512 CPU expert-path GEMV (matmul_avx.cpp:54-100,
@@ -333,6 +388,17 @@ def main():
                                       GBps=round(r["gbs"], 1),
                                       frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4)))
                 torch.cuda.empty_cache()
+        ex = None
+        for T in (64, 1024):
+            log(f"NVFP4 MoE T={T}")
+            r, ex = bench_moe(T, max(10, K // 10), 3, gen, ex)
+            secondary.append(dict(config=f"NVFP4 MoE 256 experts top-8 7168/2048 T={T} "
+                                         "(synthetic codes)", T=T, ms=round(r["ms"], 4),
+                                  experts_hit=r["experts_hit"], GBps=round(r["gbs"], 1),
+                                  frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4),
+                                  TFLOPS=round(r["tflops"], 1)))
+        del ex
+        torch.cuda.empty_cache()
         for (M, N, Kd) in [(2048, 14336, 4096), (2048, 4096, 14336)]:
             log(f"FP8 GEMM {M}x{N}x{Kd}")
             r = bench_fp8(M, N, Kd, gen, max(10, K // 10), 3)

@@ -100,17 +100,18 @@ struct XItem<TITAN_FP32> {
     TQ_DEV uint4 h() const { return make_uint4(cv(a.x, a.y), cv(a.z, a.w), cv(b.x, b.y), cv(b.z, b.w)); }
 };
 
-// TM tokens per pass, SL columns per LDS slab (TM * SL = 8192 elements, so
-// every thread stages 4 items of 8 elements per slab).  GATED: gate and up
-// together with the SwiGLU epilogue; otherwise one matrix, fp32 rows out.
-template <int TM, int SL, bool GATED, int XDT>
+// TM tokens per pass, SL columns per LDS slab, RT 16-row tiles per wave (a
+// workgroup covers 64 RT rows and stages the tokens' activations once for
+// all of them).  GATED: gate and up together with the SwiGLU epilogue;
+// otherwise one matrix, fp32 rows out.
+template <int TM, int SL, int RT, bool GATED, int XDT>
 __global__ __launch_bounds__(kMoeThreads) void moe_gemm_kernel(MoeGemmArgs a) {
     constexpr int NB = TM / 16;         // MFMA token blocks
     constexpr int CPS = SL / 128;       // 64-byte chunks per slab
     constexpr int LDR = SL + 8;         // halves per LDS row (16 B pad)
     constexpr int NI = TM * SL / 8 / kMoeThreads;
     constexpr int NM = GATED ? 2 : 1;
-    static_assert(NI == 4, "staging geometry");
+    static_assert(NI >= 1 && TM * SL == NI * 8 * kMoeThreads, "staging geometry");
     __shared__ __attribute__((aligned(16))) _Float16 xs[2][TM * LDR];
 
     const int e = blockIdx.y;
@@ -119,13 +120,18 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemm_kernel(MoeGemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane >> 4, r = lane & 15;
-    const int row0 = blockIdx.x * kMoeRowsPerWg + wave * 16;
     const titan_nvfp4_expert ex = a.experts[e];
     const uint8_t* W[2] = {(const uint8_t*)(GATED ? ex.gate : ex.down), (const uint8_t*)ex.up};
     const float gsc[2] = {GATED ? ex.gate_scale : ex.down_scale, ex.up_scale};
     const Geo geo = make_geo(TITAN_NVFP4, a.N, a.K, 16);
-    const uint32_t code_off = (uint32_t)tiled_code_off(geo, row0 + r, 0, j);
-    const uint32_t sc_off = (uint32_t)tiled_nvs_off(geo, row0 + r, 0);
+    // tile q of this wave: rows [row0(q), row0(q) + 16)
+    auto row0 = [&](int q) { return blockIdx.x * (kMoeRowsPerWg * RT) + q * kMoeRowsPerWg + wave * 16; };
+    uint32_t code_off[RT], sc_off[RT];
+#pragma unroll
+    for (int q = 0; q < RT; q++) {
+        code_off[q] = (uint32_t)tiled_code_off(geo, row0(q) + r, 0, j);
+        sc_off[q] = (uint32_t)tiled_nvs_off(geo, row0(q) + r, 0);
+    }
     const int nslab = a.K / SL;
     const int sh = 8 * (j >> 1);  // byte of the lane's scale within a half chunk
 
@@ -149,86 +155,108 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemm_kernel(MoeGemmArgs a) {
                 else xr[it].zero();
             }
         };
-        struct WSet { uint4 c[NM][CPS]; uint2 s[NM][CPS]; };
+        struct WSet { uint4 c[NM][RT][CPS]; uint2 s[NM][RT][CPS]; };
         auto load_w = [&](int s, WSet& w) {
 #pragma unroll
             for (int m = 0; m < NM; m++)
 #pragma unroll
-                for (int c = 0; c < CPS; c++) {
-                    const uint32_t ch = (uint32_t)(s * CPS + c);
-                    w.c[m][c] = *(const uint4*)(W[m] + code_off + ch * 1024u);
-                    w.s[m][c] = *(const uint2*)(W[m] + sc_off + ch * 128u);
-                }
+                for (int q = 0; q < RT; q++)
+#pragma unroll
+                    for (int c = 0; c < CPS; c++) {
+                        const uint32_t ch = (uint32_t)(s * CPS + c);
+                        w.c[m][q][c] = *(const uint4*)(W[m] + code_off[q] + ch * 1024u);
+                        w.s[m][q][c] = *(const uint2*)(W[m] + sc_off[q] + ch * 128u);
+                    }
         };
 
-        mf4 acc[NM][NB];
+        mf4 acc[NM][RT][NB];
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
-            for (int b = 0; b < NB; b++) acc[m][b] = mf4{0, 0, 0, 0};
+            for (int q = 0; q < RT; q++)
+#pragma unroll
+                for (int b = 0; b < NB; b++) acc[m][q][b] = mf4{0, 0, 0, 0};
 
+        // Software pipeline over K slabs: weights two slabs ahead in three
+        // register sets (no copies), activations one slab ahead.  Issue order
+        // per slab -- activations, then weights -- lets the wait for the
+        // activations of slab s leave the weights of slabs s+1, s+2 in flight.
         XItem<XDT> xr[NI];
-        WSet wc, wn;
-        load_w(0, wc);
+        WSet w0, w1, w2;
         load_x(0, xr);
-        for (int s = 0; s < nslab; s++) {
+        load_w(0, w0);
+        if (nslab > 1) load_w(1, w1);
+        auto step = [&](int s, const WSet& wc, WSet& wnext2) {
             _Float16* buf = xs[s & 1];
 #pragma unroll
             for (int it = 0; it < NI; it++) *(uint4*)(buf + ldsi[it]) = xr[it].h();
-            if (s + 1 < nslab) {
-                load_w(s + 1, wn);
-                load_x(s + 1, xr);
-            }
+            if (s + 1 < nslab) load_x(s + 1, xr);
+            if (s + 2 < nslab) load_w(s + 2, wnext2);
             __syncthreads();
 #pragma unroll
             for (int c = 0; c < CPS; c++) {
-                uint32_t scw[NM][4];
+                uint32_t scw[NM][RT][4];
 #pragma unroll
-                for (int m = 0; m < NM; m++) {
-                    scw[m][0] = e4m3_h16_scaled((wc.s[m][c].x >> sh) & 0xFFu);
-                    scw[m][1] = e4m3_h16_scaled((wc.s[m][c].x >> (16 + sh)) & 0xFFu);
-                    scw[m][2] = e4m3_h16_scaled((wc.s[m][c].y >> sh) & 0xFFu);
-                    scw[m][3] = e4m3_h16_scaled((wc.s[m][c].y >> (16 + sh)) & 0xFFu);
-                }
+                for (int m = 0; m < NM; m++)
+#pragma unroll
+                    for (int q = 0; q < RT; q++) {
+                        const uint2 sv = wc.s[m][q][c];
+                        scw[m][q][0] = e4m3_h16_scaled((sv.x >> sh) & 0xFFu);
+                        scw[m][q][1] = e4m3_h16_scaled((sv.x >> (16 + sh)) & 0xFFu);
+                        scw[m][q][2] = e4m3_h16_scaled((sv.y >> sh) & 0xFFu);
+                        scw[m][q][3] = e4m3_h16_scaled((sv.y >> (16 + sh)) & 0xFFu);
+                    }
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    mh8 B[NM];
+                    mh8 B[NM][RT];
 #pragma unroll
-                    for (int m = 0; m < NM; m++) {
-                        const uint4 cw = wc.c[m][c];
-                        const uint32_t w = i == 0 ? cw.x : i == 1 ? cw.y : i == 2 ? cw.z : cw.w;
-                        B[m] = nvfp4_b8(w, scw[m][i]);
-                    }
+                    for (int m = 0; m < NM; m++)
+#pragma unroll
+                        for (int q = 0; q < RT; q++) {
+                            const uint4 cw = wc.c[m][q][c];
+                            const uint32_t w = i == 0 ? cw.x : i == 1 ? cw.y : i == 2 ? cw.z : cw.w;
+                            B[m][q] = nvfp4_b8(w, scw[m][q][i]);
+                        }
 #pragma unroll
                     for (int b = 0; b < NB; b++) {
                         if (b < nb) {
                             const mh8 A = *(const mh8*)(buf + (b * 16 + r) * LDR + c * 128 + 32 * i + 8 * j);
 #pragma unroll
                             for (int m = 0; m < NM; m++)
-                                acc[m][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[m], acc[m][b], 0, 0, 0);
+#pragma unroll
+                                for (int q = 0; q < RT; q++)
+                                    acc[m][q][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                        A, B[m][q], acc[m][q][b], 0, 0, 0);
                         }
                     }
                 }
             }
-            wc = wn;
+        };
+        for (int s = 0; s < nslab; s += 3) {
+            step(s, w0, w2);
+            if (s + 1 < nslab) step(s + 1, w1, w0);
+            if (s + 2 < nslab) step(s + 2, w2, w1);
         }
 
-        // epilogue: lane holds weight row row0 + r for tokens 16 b + 4 j + v
-        const int row = row0 + r;
+        // epilogue: lane holds weight row row0(q) + r for tokens 16 b + 4 j + v
 #pragma unroll
-        for (int b = 0; b < NB; b++) {
-            if (b >= nb) break;
+        for (int q = 0; q < RT; q++) {
+            const int row = row0(q) + r;
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int tok = b * 16 + 4 * j + v;
-                if (tok >= nt) continue;
-                const int64_t o = (int64_t)(beg + t0 + tok) * a.ldo + row;
-                if constexpr (GATED) {
-                    const float g = acc[0][b][v] * gsc[0], u = acc[1][b][v] * gsc[1];
-                    const float act = (g * (1.0f / (1.0f + expf(-g)))) * u;
-                    ((_Float16*)a.out)[o] = (_Float16)act;
-                } else {
-                    ((float*)a.out)[o] = acc[0][b][v] * gsc[0];
+            for (int b = 0; b < NB; b++) {
+                if (b >= nb) break;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int tok = b * 16 + 4 * j + v;
+                    if (tok >= nt) continue;
+                    const int64_t o = (int64_t)(beg + t0 + tok) * a.ldo + row;
+                    if constexpr (GATED) {
+                        const float g = acc[0][q][b][v] * gsc[0], u = acc[1][q][b][v] * gsc[1];
+                        const float act = (g * (1.0f / (1.0f + expf(-g)))) * u;
+                        ((_Float16*)a.out)[o] = (_Float16)act;
+                    } else {
+                        ((float*)a.out)[o] = acc[0][q][b][v] * gsc[0];
+                    }
                 }
             }
         }
@@ -344,28 +372,64 @@ MoeWs carve(void* base, int tokens, int k, int E, int hidden, int inter) {
     return w;
 }
 
-template <int TM, int SL, bool GATED>
+template <int TM, int SL, int RT, bool GATED>
 int launch_moe(const MoeGemmArgs& a, int x_dtype, int E, hipStream_t st) {
-    dim3 grid(a.N / kMoeRowsPerWg, E);
+    if (a.N % (kMoeRowsPerWg * RT)) return TITAN_ERR_UNSUPPORTED;
+    dim3 grid(a.N / (kMoeRowsPerWg * RT), E);
     switch (x_dtype) {
         case TITAN_FP16:
-            hipLaunchKernelGGL((moe_gemm_kernel<TM, SL, GATED, TITAN_FP16>), grid, dim3(kMoeThreads), 0, st, a);
+            hipLaunchKernelGGL((moe_gemm_kernel<TM, SL, RT, GATED, TITAN_FP16>), grid, dim3(kMoeThreads), 0, st, a);
             break;
         case TITAN_BF16:
-            hipLaunchKernelGGL((moe_gemm_kernel<TM, SL, GATED, TITAN_BF16>), grid, dim3(kMoeThreads), 0, st, a);
+            hipLaunchKernelGGL((moe_gemm_kernel<TM, SL, RT, GATED, TITAN_BF16>), grid, dim3(kMoeThreads), 0, st, a);
             break;
         default:
-            hipLaunchKernelGGL((moe_gemm_kernel<TM, SL, GATED, TITAN_FP32>), grid, dim3(kMoeThreads), 0, st, a);
+            hipLaunchKernelGGL((moe_gemm_kernel<TM, SL, RT, GATED, TITAN_FP32>), grid, dim3(kMoeThreads), 0, st, a);
             break;
     }
     return tqh::launch_status();
 }
 
+// Tokens per pass from the mean load per expert; more rows per workgroup as
+// the token tile grows, so that the activation staging stays small next to
+// the weight stream.
+// (tokens per pass, LDS slab columns, row tiles per wave) per token tile
+#ifndef TQ_MOE_G16
+#define TQ_MOE_G16 16, 128, 2
+#endif
+#ifndef TQ_MOE_D16
+#define TQ_MOE_D16 16, 128, 2
+#endif
+#ifndef TQ_MOE_G32
+#define TQ_MOE_G32 32, 128, 2
+#endif
+#ifndef TQ_MOE_D32
+#define TQ_MOE_D32 32, 128, 2
+#endif
+#ifndef TQ_MOE_G64
+#define TQ_MOE_G64 64, 128, 2
+#endif
+#ifndef TQ_MOE_D64
+#define TQ_MOE_D64 64, 128, 4
+#endif
+#ifndef TQ_MOE_T32
+#define TQ_MOE_T32 8   // mean tokens per expert above which 32-token passes are used
+#endif
+#ifndef TQ_MOE_T64
+#define TQ_MOE_T64 24  // ... and 64-token passes
+#endif
+
 template <bool GATED>
 int launch_moe_tm(int tm, const MoeGemmArgs& a, int x_dtype, int E, hipStream_t st) {
-    if (tm == 16) return launch_moe<16, 512, GATED>(a, x_dtype, E, st);
-    if (tm == 32) return launch_moe<32, 256, GATED>(a, x_dtype, E, st);
-    return launch_moe<64, 128, GATED>(a, x_dtype, E, st);
+    if constexpr (GATED) {
+        if (tm == 16) return launch_moe<TQ_MOE_G16, true>(a, x_dtype, E, st);
+        if (tm == 32) return launch_moe<TQ_MOE_G32, true>(a, x_dtype, E, st);
+        return launch_moe<TQ_MOE_G64, true>(a, x_dtype, E, st);
+    } else {
+        if (tm == 16) return launch_moe<TQ_MOE_D16, false>(a, x_dtype, E, st);
+        if (tm == 32) return launch_moe<TQ_MOE_D32, false>(a, x_dtype, E, st);
+        return launch_moe<TQ_MOE_D64, false>(a, x_dtype, E, st);
+    }
 }
 
 }  // namespace
@@ -404,7 +468,7 @@ extern "C" int titan_moe_nvfp4_forward(const titan_nvfp4_expert* experts, int nu
 
     // tokens per pass from the mean load per expert
     const int avg = (P + num_experts - 1) / num_experts;
-    const int tm = avg <= 8 ? 16 : avg <= 24 ? 32 : 64;
+    const int tm = avg <= TQ_MOE_T32 ? 16 : avg <= TQ_MOE_T64 ? 32 : 64;
 
     MoeGemmArgs g{};
     g.experts = experts;
