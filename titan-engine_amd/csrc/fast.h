@@ -256,14 +256,7 @@ struct FxNib {
             const int i = g * GS;
             const float s = d.s[i] * kTwo24, sh = d.s[i] * (kTwo24 / 16.0f), bb = d.b[i];
             float4 xs;
-            if constexpr (SX) {  // sums of the group's columns for tokens 0..3
-                xs = *(const float4*)(sx + 4 * i);
-#pragma unroll
-                for (int q = 1; q < GS; q++) {
-                    const float4 t = *(const float4*)(sx + 4 * (i + q));
-                    xs.x += t.x; xs.y += t.y; xs.z += t.z; xs.w += t.w;
-                }
-            }
+            if constexpr (SX) xs = *(const float4*)(sx + 4 * i);  // the group's column sums
 #pragma unroll
             for (int n = 0; n < NB; n++)
 #pragma unroll
@@ -285,6 +278,8 @@ struct FxNib {
         return pack8(o);
     }
     TQ_DEV static int steps_per_group(const WDesc& w) { return w.g.gs >= 128 ? 4 : w.g.gs / 32; }
+    // columns summed per activation-sum entry (SX): one scale group
+    template <int GS> static constexpr int sx_cols() { return 32 * GS; }
 };
 template <int L> using FxInt4 = FxNib<L, false>;
 template <int L> using FxFp4 = FxNib<L, true>;
@@ -427,15 +422,8 @@ struct FxInt2 {
         for (int g = 0; g < 4 / GS; g++) {
             const int i = g * GS;
             const float s = d.s[i] * kTwo24, bb = d.b[i];
-            float4 xs;
-            if constexpr (SX) {  // a word step is 64 columns: two 32-column sums
-                xs = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (int q = 0; q < 2 * GS; q++) {
-                    const float4 t = *(const float4*)(sx + 4 * (2 * i + q));
-                    xs.x += t.x; xs.y += t.y; xs.z += t.z; xs.w += t.w;
-                }
-            }
+            float4 xs;  // the group's column sums (a word step is 64 columns)
+            if constexpr (SX) xs = *(const float4*)(sx + 4 * (2 * i));
 #pragma unroll
             for (int n = 0; n < NB; n++)
 #pragma unroll
@@ -458,6 +446,7 @@ struct FxInt2 {
         return pack8(o);
     }
     TQ_DEV static int steps_per_group(const WDesc& w) { return w.g.gs >= 256 ? 4 : w.g.gs / 64; }
+    template <int GS> static constexpr int sx_cols() { return 64 * GS; }
 };
 
 // ============================================================================
@@ -543,6 +532,7 @@ struct FxNvfp4 {
     TQ_DEV static void finish(const Tmp<NB, GS, SX>&, const Dec&, const float*, f4_t*) {}
     TQ_DEV static uint4 stage8(const _Float16* xr, int d0) { return FxNib<LAYOUT>::stage8(xr, d0); }
     TQ_DEV static int steps_per_group(const WDesc&) { return 1; }
+    template <int GS> static constexpr int sx_cols() { return 32; }
 };
 
 // ============================================================================
@@ -702,6 +692,7 @@ struct FxQ4K {
         return pack8(o);
     }
     TQ_DEV static int steps_per_group(const WDesc&) { return 2; }
+    template <int GS> static constexpr int sx_cols() { return 32; }
 };
 
 // ============================================================================
@@ -815,6 +806,7 @@ struct FxQ3K {
         return pack8(o);
     }
     TQ_DEV static int steps_per_group(const WDesc&) { return 1; }
+    template <int GS> static constexpr int sx_cols() { return 32; }
 };
 
 // ============================================================================
@@ -885,6 +877,7 @@ struct FxFp8 {
         return pack8(o);
     }
     TQ_DEV static int steps_per_group(const WDesc&) { return 1; }
+    template <int GS> static constexpr int sx_cols() { return 32; }
 };
 
 }  // namespace tq

@@ -25,7 +25,16 @@ namespace tq {
 #endif
 constexpr int kGemvWaves = 4;
 constexpr int kGemvThreads = kGemvWaves * kWave;
-constexpr int kGemvLdsBytes = 32 * 1024;  // activation stage per workgroup
+#ifndef TQ_GEMV_LDS_KB
+#define TQ_GEMV_LDS_KB 32
+#endif
+#ifndef TQ_GEMV_WAVES_TARGET
+#define TQ_GEMV_WAVES_TARGET 2048
+#endif
+#ifndef TQ_GEMV_KS_MAX
+#define TQ_GEMV_KS_MAX 2
+#endif
+constexpr int kGemvLdsBytes = TQ_GEMV_LDS_KB * 1024;  // activation stage per workgroup
 
 enum { kModeF32 = 0, kModeDot2 = 1, kModeMfma = 2 };
 
@@ -77,19 +86,19 @@ TQ_DEV void stage_f32(float* xf, float* s16, int pc, const void* x, int xdt, int
 
 // fp16 activations in the format's pairing order (F::stage8) and, for the
 // VALU fold, fp32 sums of every 16 columns.  Rows of x are 16-byte aligned.
-// SX (MFMA with at most 4 tokens): fp32 sums of every 32 columns for token
-// slots 0..3 at s16[4 * (col / 32) + token].
-template <int M>
-TQ_DEV void stage_sums32(float* sx, const void* x, int64_t ldx, int m0, int mcount, int col0,
-                         int ncols, int tid) {
-    for (int e = tid; e < 4 * (ncols >> 5); e += kGemvThreads) {
+// SX (MFMA with at most 4 tokens): fp32 sums of the activations over every
+// SW columns (one scale group, or one 32-column sub-block), token slots 0..3,
+// at s16[4 * (col / 32) + token] for the first column of each span.
+template <int M, int SW>
+TQ_DEV void stage_sums(float* sx, const void* x, int64_t ldx, int m0, int mcount, int col0,
+                       int ncols, int tid) {
+    for (int e = tid; e < 4 * (ncols / SW); e += kGemvThreads) {
         const int b = e >> 2, m = e & 3;
         float s = 0.0f;
         if (m < mcount && m < M) {
-            const _Float16* src = (const _Float16*)x + (int64_t)(m0 + m) * ldx + col0 + 32 * b;
+            const _Float16* src = (const _Float16*)x + (int64_t)(m0 + m) * ldx + col0 + SW * b;
             float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 32; q += 8) {
+            for (int q = 0; q < SW; q += 8) {
                 _Float16 h[8];
                 ldh8(src + q, h);
 #pragma unroll
@@ -100,7 +109,7 @@ TQ_DEV void stage_sums32(float* sx, const void* x, int64_t ldx, int m0, int mcou
             }
             s = a0 + a1;
         }
-        sx[e] = s;
+        sx[4 * (b * (SW / 32)) + m] = s;
     }
 }
 
@@ -134,6 +143,11 @@ TQ_DEV void stage_f16(_Float16* xh, float* s16, int pc, const void* x, int64_t l
         }
     }
 }
+
+// chunks per load group (a larger group needs a proportionally larger
+// activation stage, which costs more in occupancy than it gains)
+template <class F, int M, int MODE>
+constexpr int gemv_u() { return TQ_GEMV_U; }
 
 template <class F, int M, int MODE, int GS = 4>
 __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
@@ -175,7 +189,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     // flight while the current group is folded.  Every wave runs the same
     // number of groups (chunks past the end are masked) so the staging
     // barriers line up.
-    constexpr int U = TQ_GEMV_U;
+    constexpr int U = gemv_u<F, M, MODE>();
     // chunks per phase: the LDS stage (pc columns) or the whole row, in
     // whole rounds of U chunks for each of the KS waves
     const int round = U << ks_log;
@@ -204,7 +218,8 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
                 stage_f32<M>(xf, s16, pc, P.x, a.xdt, P.ldx, a.m0, a.mcount, col0, ncols, tid);
             else
                 stage_f16<F, M, MODE == kModeDot2>(xh, s16, pc, P.x, P.ldx, a.m0, a.mcount, col0, ncols, tid);
-            if constexpr (SX) stage_sums32<M>(s16, P.x, P.ldx, a.m0, a.mcount, col0, ncols, tid);
+            if constexpr (SX)
+                stage_sums<M, F::template sx_cols<GS>()>(s16, P.x, P.ldx, a.m0, a.mcount, col0, ncols, tid);
             __syncthreads();
         }
         if constexpr (MODE == kModeMfma) {
@@ -392,16 +407,16 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
     // (target: about 2048 waves in flight, at least 8 chunks per wave)
     long long work = 0;
     for (int i = 0; i < a.n; i++) work += (long long)a.p[i].ntiles * a.p[i].nchunks;
-    const long long target = work / 2048 > 8 ? work / 2048 : 8;
+    const long long target = work / TQ_GEMV_WAVES_TARGET > 8 ? work / TQ_GEMV_WAVES_TARGET : 8;
     for (int i = 0; i < a.n; i++) {
         int ks = 0;
-        while (ks < 2 && a.p[i].nchunks > target << ks) ks++;
+        while (ks < TQ_GEMV_KS_MAX && a.p[i].nchunks > target << ks) ks++;
         a.p[i].ks_log = ks;
     }
     // phase width: whole rounds of 4 waves x U = 4 chunks, at most
     // kGemvLdsBytes of staged activations (at least one round), no wider
     // than the longest row
-    const int step = 16 * F::CHUNK_COLS;
+    const int step = kGemvWaves * gemv_u<F, M, MODE>() * F::CHUNK_COLS;
     int maxcols = 0;
     for (int i = 0; i < a.n; i++) maxcols = maxcols > a.p[i].w.g.cols ? maxcols : a.p[i].w.g.cols;
     // bytes per column per token, x4: fp32 + sums 17, fp16 + sums 9, fp16 8
