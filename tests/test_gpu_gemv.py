@@ -178,3 +178,40 @@ def test_batched_launch_matches_single(lay, rng):
         for d, X, Y in zip(ds, Xs, Ys):
             ref = X.double().cpu().numpy() @ d["deq"].astype(np.float64).T
             assert_close_out(to_np(Y), ref, "f16")
+
+
+@pytest.mark.parametrize("M", [8, 16, 24, 32, 50, 64, 100])
+@pytest.mark.parametrize("rows,cols,gs", [(64, 512, 128), (80, 384, 32), (208, 1024, 64),
+                                          (128, 768, 256)])
+def test_int4_token_tiled_parity(M, rows, cols, gs, rng):
+    """INT4 tiled with M >= 8 runs the token-tiled dequant-GEMM (partial row
+    blocks, every group size class, token tiles of 16/32/64 and several tiles)."""
+    d = make_weights("int4", rows, cols, rng, gs=gs)
+    W = upload(d, tq.LAYOUT_TILED)
+    for xdt, ydt in [("f16", "f16"), ("bf16", "f32"), ("f32", "bf16")]:
+        x, x64 = act(M, cols, xdt, rng)
+        y = tq.qgemm(W, x, out_dtype=TDT[ydt])
+        torch.cuda.synchronize()
+        assert_close_out(to_np(y), x64 @ d["deq"].astype(np.float64).T, ydt)
+
+
+def test_int4_token_tiled_batched_strided(rng):
+    """Batched problems of different shapes share one launch; padded strides."""
+    shapes = [(64, 512), (16, 512), (112, 1024)]
+    ds = [make_weights("int4", r, c, rng, gs=128) for r, c in shapes]
+    Ws = [upload(d, tq.LAYOUT_TILED) for d in ds]
+    M = 40
+    Xs = [act(M, c, "f16", rng) for _, c in shapes]
+    Ys = [torch.empty(M, r, dtype=torch.float16, device="cuda") for r, _ in shapes]
+    tq.qgemm_batched(Ws, [x for x, _ in Xs], Ys)
+    torch.cuda.synchronize()
+    for d, (x, x64), y in zip(ds, Xs, Ys):
+        assert_close_out(to_np(y), x64 @ d["deq"].astype(np.float64).T, "f16")
+    d = ds[0]
+    xfull = torch.randn(M, 512 + 56, dtype=torch.float16, device="cuda")
+    yfull = torch.zeros(M, 64 + 8, dtype=torch.float32, device="cuda")
+    tq.qgemm(Ws[0], xfull[:, :512], out=yfull[:, :64])
+    torch.cuda.synchronize()
+    ref = xfull[:, :512].double().cpu().numpy() @ d["deq"].astype(np.float64).T
+    assert_close_out(to_np(yfull[:, :64]), ref, "f32")
+    assert torch.all(yfull[:, 64:] == 0)

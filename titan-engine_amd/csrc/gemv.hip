@@ -1,11 +1,18 @@
 // gemv.hip -- host side of the dequant-GEMV path (validation, batching,
 // C ABI).  Kernels live in gemv_impl.h, instantiated by gemv_fmt_*.hip.
 #include "gemv_impl.h"
+#include "qgemm_tok.h"
 
 // ============================================================================
 // Host side
 // ============================================================================
 namespace {
+
+#ifndef TQ_TOK_MIN
+#define TQ_TOK_MIN 8
+#endif
+// token count from which INT4 tiled weights go to the token-tiled kernel
+constexpr int kTokMinTokens = TQ_TOK_MIN;
 
 using namespace tq;
 
@@ -146,6 +153,9 @@ int run_gemv(const titan_qweight* Ws, const void* const* Xs, const int64_t* ldx,
         }
         return tqh::launch_status();
     }
+    // several tokens of INT4 tiled weights: the token-tiled dequant-GEMM
+    if (M >= kTokMinTokens && tqh::tok_int4_ok(Ws, Xs, ldx, n, xdt))
+        return tqh::run_tok_int4(Ws, Xs, ldx, Ys, ldy, n, xdt, ydt, M, st);
     bool has_mfma = false;
     switch (fmt) {
         case TITAN_INT4: has_mfma = gemv_has_mfma_int4(); break;

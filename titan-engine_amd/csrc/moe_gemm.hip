@@ -23,6 +23,7 @@
 // fp16 normal range); the fp32 global scale multiplies the accumulator.
 #include "common.h"
 #include "layout.h"
+#include "xitem.h"
 
 namespace tq {
 
@@ -63,42 +64,6 @@ TQ_DEV mh8 nvfp4_b8(uint32_t w, uint32_t sc16) {
     const mh2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 256.0f, 3) * s;
     return mh8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
-
-// 8 activation elements of one source dtype, converted to fp16 for LDS.
-template <int XDT>
-struct XItem;
-template <>
-struct XItem<TITAN_FP16> {
-    uint4 a;
-    TQ_DEV void load(const void* p, int64_t e) { a = *(const uint4*)((const uint16_t*)p + e); }
-    TQ_DEV void zero() { a = make_uint4(0, 0, 0, 0); }
-    TQ_DEV uint4 h() const { return a; }
-};
-template <>
-struct XItem<TITAN_BF16> {
-    uint4 a;
-    TQ_DEV void load(const void* p, int64_t e) { a = *(const uint4*)((const uint16_t*)p + e); }
-    TQ_DEV void zero() { a = make_uint4(0, 0, 0, 0); }
-    TQ_DEV static uint32_t cv(uint32_t w) {
-        const mh2 v = {(_Float16)bf16_to_f32(w & 0xFFFFu), (_Float16)bf16_to_f32(w >> 16)};
-        return __builtin_bit_cast(uint32_t, v);
-    }
-    TQ_DEV uint4 h() const { return make_uint4(cv(a.x), cv(a.y), cv(a.z), cv(a.w)); }
-};
-template <>
-struct XItem<TITAN_FP32> {
-    float4 a, b;
-    TQ_DEV void load(const void* p, int64_t e) {
-        a = *(const float4*)((const float*)p + e);
-        b = *(const float4*)((const float*)p + e + 4);
-    }
-    TQ_DEV void zero() { a = b = make_float4(0, 0, 0, 0); }
-    TQ_DEV static uint32_t cv(float x, float y) {
-        const mh2 v = {(_Float16)x, (_Float16)y};
-        return __builtin_bit_cast(uint32_t, v);
-    }
-    TQ_DEV uint4 h() const { return make_uint4(cv(a.x, a.y), cv(a.z, a.w), cv(b.x, b.y), cv(b.z, b.w)); }
-};
 
 // TM tokens per pass, SL columns per LDS slab, RT 16-row tiles per wave (a
 // workgroup covers 64 RT rows and stages the tokens' activations once for
