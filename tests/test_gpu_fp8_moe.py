@@ -16,14 +16,18 @@ def bf16_bits(t):
     return t.cpu().view(torch.int16).numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("M,K", [(1, 256), (7, 4096), (64, 1000)])
-def test_fp8_quantize_rows_bit_exact(M, K):
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("M,K", [(1, 256), (7, 4096), (64, 1000), (5, 1003)])
+def test_fp8_quantize_rows_bit_exact(M, K, dt):
+    # bf16 values are exact in fp16 (|x| > 2^-14 here) and fp32, so every
+    # input dtype has the same answer; K = 1003 takes the unvectorised path
     g = torch.Generator().manual_seed(M * 7 + K)
     x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    x[x.abs() < 2 ** -12] = 0
     x[0, :5] = 0  # partial zeros; an all-zero row below
     if M > 2:
         x[2] = 0
-    xd = x.cuda()
+    xd = x.to({"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dt]).cuda()
     xq = torch.empty(M, K, dtype=torch.uint8, device="cuda")
     xs = torch.empty(M, dtype=torch.float32, device="cuda")
     tq.fp8_quantize_rows(xd, xq, xs)

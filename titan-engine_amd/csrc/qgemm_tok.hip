@@ -300,8 +300,14 @@ int run_tok_int4(const titan_qweight* Ws, const void* const* Xs, const int64_t* 
     const int gs = Ws[0].group_size;
     const int fw = gs >= 128 ? 4 : gs / 32;
     // token tile: the fewest 16-token blocks that cover M in one tile, up to 64
-    if (M <= 16) tq::launch_tok_f<16, 4>(a, maxrows, fw, xdt, ydt, st);
-    else if (M <= 32) tq::launch_tok_f<32, 2>(a, maxrows, fw, xdt, ydt, st);
+#ifndef TQ_TOK_T16
+#define TQ_TOK_T16 64     // largest M served by 16-token tiles (one tile per 16 tokens)
+#endif
+#ifndef TQ_TOK_RT32
+#define TQ_TOK_RT32 2
+#endif
+    if (M <= TQ_TOK_T16) tq::launch_tok_f<16, 4>(a, maxrows, fw, xdt, ydt, st);
+    else if (M <= 32) tq::launch_tok_f<32, TQ_TOK_RT32>(a, maxrows, fw, xdt, ydt, st);
     else tq::launch_tok_f<64, 2>(a, maxrows, fw, xdt, ydt, st);
     return launch_status();
 }
