@@ -144,43 +144,92 @@ __global__ __launch_bounds__(128 * WGN) void fp8_gemm_kernel(const uint8_t* __re
     // kt + S, and reads stage kt + 1's fragments while stage kt's
     // matrix-core instructions run -- so after each barrier the matrix cores
     // restart at once, with no LDS latency in front of them.
-    v8i fa[2][TI], fb[2][TJ];  // ping-pong fragment sets (indices fold to registers)
-    auto read_frags = [&](int kt, v8i* a, v8i* b) {
-        const uint8_t* st = sm + (kt % S) * SBYTES;
+    if constexpr (TJ <= 2) {
+        // two waves per SIMD: every fragment of stage kt + 1 is read while
+        // stage kt's matrix-core instructions run; stage kt's buffer is
+        // refilled with stage kt + S as soon as the barrier has passed
+        v8i fa[2][TI], fb[2][TJ];  // ping-pong fragment sets (indices fold to registers)
+        auto read_frags = [&](int kt, v8i* a, v8i* b) {
+            const uint8_t* st = sm + (kt % S) * SBYTES;
 #pragma unroll
-        for (int jn = 0; jn < TJ; jn++) b[jn] = frag(st + ABYTES + (wn * TJ + jn) * 2048);
+            for (int jn = 0; jn < TJ; jn++) b[jn] = frag(st + ABYTES + (wn * TJ + jn) * 2048);
 #pragma unroll
-        for (int i = 0; i < TI; i++) a[i] = frag(st + (wm * TI + i) * 2048);
-    };
+            for (int i = 0; i < TI; i++) a[i] = frag(st + (wm * TI + i) * 2048);
+        };
 #pragma unroll
-    for (int kt = 0; kt < S; kt++)
-        if (kt < nk) issue(kt);
-    // stage 0 landed: at most stages 1 .. min(S, nk) - 1 outstanding
-    if (nk >= S) __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 1) * LPW));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-    wg_barrier();
-    read_frags(0, fa[0], fb[0]);
-    for (int k2 = 0; k2 < nk; k2 += 2) {
+        for (int kt = 0; kt < S; kt++)
+            if (kt < nk) issue(kt);
+        // stage 0 landed: at most stages 1 .. min(S, nk) - 1 outstanding
+        if (nk >= S) __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 1) * LPW));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+        wg_barrier();
+        read_frags(0, fa[0], fb[0]);
+        for (int k2 = 0; k2 < nk; k2 += 2) {
 #pragma unroll
-        for (int ph = 0; ph < 2; ph++) {
-            const int kt = k2 + ph;
-            if (kt >= nk) break;
-            // stages issued after kt + 1: kt + 2 .. min(kt + S - 1, nk - 1)
-            if (kt + S - 1 < nk) __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 2) * LPW));
-            else if (kt + S - 2 < nk) __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 3) * LPW));
+            for (int ph = 0; ph < 2; ph++) {
+                const int kt = k2 + ph;
+                if (kt >= nk) break;
+                // stages issued after kt + 1: kt + 2 .. min(kt + S - 1, nk - 1)
+                if (kt + S - 1 < nk) __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 2) * LPW));
+                else if (kt + S - 2 < nk) __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 3) * LPW));
+                else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+                wg_barrier();  // stage kt + 1 landed everywhere; stage kt's buffer is free
+    #ifndef TQ_EXP_NOLOAD
+                if (kt + S < nk) issue(kt + S);
+    #endif
+                // past the last stage this reads a stale buffer; the values are unused
+                read_frags(kt + 1, fa[ph ^ 1], fb[ph ^ 1]);
+#pragma unroll
+                for (int jn = 0; jn < TJ; jn++) {
+#pragma unroll
+                    for (int i = 0; i < TI; i++)
+                        acc[i][jn] = mfma_fp8_32(fa[ph][i], fb[ph][jn], acc[i][jn]);
+                }
+            }
+        }
+    } else {
+        // one wave per SIMD (large wave tile, fewer LDS reads): this stage's
+        // B fragments stream one ahead of their matrix-core instructions and
+        // the next stage's A fragments and first B fragment are read under
+        // the last ones; stage kt - 1's buffer is refilled with stage kt + S - 1
+        v8i fa[TI], fan[TI], fb, fbn;
+        auto read_a = [&](int kt, v8i* a) {
+            const uint8_t* st = sm + (kt % S) * SBYTES;
+#pragma unroll
+            for (int i = 0; i < TI; i++) a[i] = frag(st + (wm * TI + i) * 2048);
+        };
+        auto b_at = [&](int kt, int jn) { return sm + (kt % S) * SBYTES + ABYTES + (wn * TJ + jn) * 2048; };
+#pragma unroll
+        for (int kt = 0; kt < S - 1; kt++)
+            if (kt < nk) issue(kt);
+        // stage 0 landed: at most stages 1 .. min(S - 1, nk) - 1 outstanding
+        if (nk >= S - 1) __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 2) * LPW));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+        wg_barrier();
+        read_a(0, fa);
+        fb = frag(b_at(0, 0));
+        for (int kt = 0; kt < nk; kt++) {
+            // stages issued after kt + 1: kt + 2 .. min(kt + S - 2, nk - 1)
+            if (kt + S - 2 < nk) __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 3) * LPW));
             else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-            wg_barrier();  // stage kt + 1 landed everywhere; stage kt's buffer is free
+            wg_barrier();  // stage kt + 1 landed everywhere; stage kt - 1's buffer is free
 #ifndef TQ_EXP_NOLOAD
-            if (kt + S < nk) issue(kt + S);
+            if (kt + S - 1 < nk) issue(kt + S - 1);
 #endif
-            // past the last stage this reads a stale buffer; the values are unused
-            read_frags(kt + 1, fa[ph ^ 1], fb[ph ^ 1]);
 #pragma unroll
             for (int jn = 0; jn < TJ; jn++) {
+                if (jn + 1 < TJ) {
+                    fbn = frag(b_at(kt, jn + 1));
+                } else {  // past the last stage: a stale buffer, values unused
+                    read_a(kt + 1, fan);
+                    fbn = frag(b_at(kt + 1, 0));
+                }
 #pragma unroll
-                for (int i = 0; i < TI; i++)
-                    acc[i][jn] = mfma_fp8_32(fa[ph][i], fb[ph][jn], acc[i][jn]);
+                for (int i = 0; i < TI; i++) acc[i][jn] = mfma_fp8_32(fa[i], fb, acc[i][jn]);
+                fb = fbn;
             }
+#pragma unroll
+            for (int i = 0; i < TI; i++) fa[i] = fan[i];
         }
     }
 
