@@ -213,9 +213,10 @@ struct FxNib {
                 const uint32_t u = w >> 8;
                 float lo = dot2(w & 0x000F000Fu, xv.x, 0.0f);  // (n0, n4)
                 lo = dot2(u & 0x000F000Fu, xv.y, lo);          // (n2, n6)
-                float hi = dot2(w & 0x00F000F0u, xv.z, 0.0f);  // (n1, n5) x16
-                hi = dot2(u & 0x00F000F0u, xv.w, hi);          // (n3, n7) x16
-                t = __builtin_fmaf(d.s[i], __builtin_fmaf(hi, 0.0625f, lo) * kTwo24, t);
+                // (n1, n5) / (n3, n7) enter x16 against activations staged / 16
+                float hi = dot2(w & 0x00F000F0u, xv.z, 0.0f);
+                hi = dot2(u & 0x00F000F0u, xv.w, hi);
+                t = __builtin_fmaf(d.s[i], (lo + hi) * kTwo24, t);
             }
         }
         return j == 0 ? t + bias(d, s16) : t;
@@ -229,23 +230,24 @@ struct FxNib {
     // 32 columns comes from LDS instead (M <= 4: only accumulator entries of
     // lanes q = 0 hold tokens).
     template <int NB, int GS, bool SX>
-    struct Tmp { f4_t C[4 / GS][NB], H[4 / GS][NB], O[SX ? 1 : 4 / GS][NB]; };
+    struct Tmp { f4_t C[4 / GS][NB], O[SX ? 1 : 4 / GS][NB]; };
     template <int NB, int GS, bool SX>
     TQ_DEV static void issue(const Raw& r, int j, const _Float16* const* xt, Tmp<NB, GS, SX>& T) {
-        const h8_t ones = h8_of(make_uint4(kOnes2, kOnes2, kOnes2, kOnes2));
+        // staged activations of a step: columns (0,4,2,6) and (1,5,3,7) / 16, so
+        // the ones vector weighs the second half by 16 for sum(x)
+        const h8_t ones = h8_of(make_uint4(kOnes2, kOnes2, 0x4C004C00u, 0x4C004C00u));
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int g = i / GS;
             const uint32_t w = r.w[i], u = w >> 8;
-            const h4_t blo = h4_of(w & 0x000F000Fu, u & 0x000F000Fu);  // (n0, n4, n2, n6)
-            const h4_t bhi = h4_of(w & 0x00F000F0u, u & 0x00F000F0u);  // (n1, n5, n3, n7) x16
+            // (n0, n4, n2, n6) and 16 x (n1, n5, n3, n7), exact fp16 subnormals
+            const h8_t b = h8_of(make_uint4(w & 0x000F000Fu, u & 0x000F000Fu, w & 0x00F000F0u, u & 0x00F000F0u));
 #pragma unroll
             for (int n = 0; n < NB; n++) {
-                const uint4 xv = *(const uint4*)(xt[n] + 32 * i + 8 * j);
+                const h8_t xv = h8_of(*(const uint4*)(xt[n] + 32 * i + 8 * j));
                 const bool first = i % GS == 0;
-                T.C[g][n] = mfma16(h4_of(xv.x, xv.y), blo, first ? f4_zero() : T.C[g][n]);
-                T.H[g][n] = mfma16(h4_of(xv.z, xv.w), bhi, first ? f4_zero() : T.H[g][n]);
-                if constexpr (!SX) T.O[g][n] = mfma32(h8_of(xv), ones, first ? f4_zero() : T.O[g][n]);
+                T.C[g][n] = mfma32(xv, b, first ? f4_zero() : T.C[g][n]);
+                if constexpr (!SX) T.O[g][n] = mfma32(xv, ones, first ? f4_zero() : T.O[g][n]);
             }
         }
     }
@@ -254,15 +256,14 @@ struct FxNib {
 #pragma unroll
         for (int g = 0; g < 4 / GS; g++) {
             const int i = g * GS;
-            const float s = d.s[i] * kTwo24, sh = d.s[i] * (kTwo24 / 16.0f), bb = d.b[i];
+            const float s = d.s[i] * kTwo24, bb = d.b[i];
             float4 xs;
             if constexpr (SX) xs = *(const float4*)(sx + 4 * i);  // the group's column sums
 #pragma unroll
             for (int n = 0; n < NB; n++)
 #pragma unroll
                 for (int v = 0; v < NV; v++) {
-                    float t = __builtin_fmaf(s, T.C[g][n][v], acc[n][v]);
-                    t = __builtin_fmaf(sh, T.H[g][n][v], t);
+                    const float t = __builtin_fmaf(s, T.C[g][n][v], acc[n][v]);
                     const float o = SX ? (v == 0 ? xs.x : v == 1 ? xs.y : v == 2 ? xs.z : xs.w)
                                        : T.O[SX ? 0 : g][n][v];
                     acc[n][v] = __builtin_fmaf(bb, o, t);
@@ -270,11 +271,15 @@ struct FxNib {
         }
     }
     // 8 staged activations starting at chunk column d0 (d0 % 8 == 0)
+    // INT4 (matrix cores): the odd columns are pre-divided by 16 to meet their
+    // codes, which enter 16x too large (exact for |x| >= 2^-10; below that the
+    // quotient is an fp16 subnormal, off by at most 2^-25)
     TQ_DEV static uint4 stage8(const _Float16* xr, int d0) {
         _Float16 h[8], o[8];
         ldh8(xr + d0, h);
+        const _Float16 k = IS_FP4 ? (_Float16)1.0f : (_Float16)0.0625f;
         o[0] = h[0]; o[1] = h[4]; o[2] = h[2]; o[3] = h[6];
-        o[4] = h[1]; o[5] = h[5]; o[6] = h[3]; o[7] = h[7];
+        o[4] = h[1] * k; o[5] = h[5] * k; o[6] = h[3] * k; o[7] = h[7] * k;
         return pack8(o);
     }
     TQ_DEV static int steps_per_group(const WDesc& w) { return w.g.gs >= 128 ? 4 : w.g.gs / 32; }
@@ -530,7 +535,7 @@ struct FxNvfp4 {
     TQ_DEV static void issue(const Raw&, int, const _Float16* const*, Tmp<NB, GS, SX>&) {}
     template <int NB, int NV, int GS, bool SX>
     TQ_DEV static void finish(const Tmp<NB, GS, SX>&, const Dec&, const float*, f4_t*) {}
-    TQ_DEV static uint4 stage8(const _Float16* xr, int d0) { return FxNib<LAYOUT>::stage8(xr, d0); }
+    TQ_DEV static uint4 stage8(const _Float16* xr, int d0) { return FxNib<LAYOUT, true>::stage8(xr, d0); }
     TQ_DEV static int steps_per_group(const WDesc&) { return 1; }
     template <int GS> static constexpr int sx_cols() { return 32; }
 };
