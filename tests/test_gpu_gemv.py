@@ -215,3 +215,23 @@ def test_int4_token_tiled_batched_strided(rng):
     ref = xfull[:, :512].double().cpu().numpy() @ d["deq"].astype(np.float64).T
     assert_close_out(to_np(yfull[:, :64]), ref, "f32")
     assert torch.all(yfull[:, 64:] == 0)
+
+
+@pytest.mark.parametrize("rows,cols,gs,nact", [(64, 512, 128, 17), (40, 1000, 40, 40), (96, 256, 64, 0)])
+def test_sparse_dequant_matvec_int4(rows, cols, gs, nact, rng):
+    """sparse.cu:142-205: only the listed rows are written (REF INT4, fp32)."""
+    d = make_weights("int4", rows, cols, rng, gs=gs)
+    active = np.sort(rng.choice(rows, size=nact, replace=False)).astype(np.int32)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    y = torch.full((rows,), 7.5, device="cuda")
+    tq.sparse_dequant_matvec_int4(dev(d["codes"]), dev(d["scales"]), dev(d["biases"]), dev(x), y,
+                                  dev(active) if nact else torch.zeros(0, dtype=torch.int32, device="cuda"),
+                                  cols, gs)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().astype(np.float64)
+    ref = d["deq"].astype(np.float64) @ x.astype(np.float64)
+    mask = np.zeros(rows, bool)
+    mask[active] = True
+    assert np.all(got[~mask] == 7.5)
+    if nact:
+        assert_close_out(got[mask], ref[mask], "f32")

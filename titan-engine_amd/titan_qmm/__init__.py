@@ -48,6 +48,7 @@ _SIGS = {
     "titan_dequant_matvec_fp4": [_P, _P, _P, _P, _I, _I, _I, _P],
     "titan_dequant_matvec_nvfp4": [_P, _P, _F, _P, _P, _I, _I, _P],
     "titan_quantize_fp4": [_P, _P, _P, _I, _I, _P],
+    "titan_sparse_dequant_matvec_int4": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "titan_qgemm": [ctypes.POINTER(QWeightC), _P, _I, _I64, _P, _I, _I64, _I, _P],
     "titan_qgemm_batched": [ctypes.POINTER(QWeightC), ctypes.POINTER(_P), ctypes.POINTER(_P),
                             _I, _I, _I, _I, _P],
@@ -250,6 +251,12 @@ def dequant_matvec_fp4(w, s, x, y, rows, cols, gs, stream=None):
 def dequant_matvec_nvfp4(w, s, g, x, y, rows, cols, stream=None):
     _check(lib().titan_dequant_matvec_nvfp4(_ptr(w), _ptr(s), float(g), _ptr(x), _ptr(y), rows,
                                             cols, _stream(stream)), "dequant_matvec_nvfp4")
+
+
+def sparse_dequant_matvec_int4(w, s, b, x, y, active, cols, gs, stream=None):
+    _check(lib().titan_sparse_dequant_matvec_int4(_ptr(w), _ptr(s), _ptr(b), _ptr(x), _ptr(y),
+                                                  _ptr(active), active.numel(), cols, gs,
+                                                  _stream(stream)), "sparse_dequant_matvec_int4")
 
 
 def quantize_fp4(x, out, scales, numel, gs, stream=None):
