@@ -174,9 +174,7 @@ __global__ __launch_bounds__(128 * WGN) void fp8_gemm_kernel(const uint8_t* __re
                 else if (kt + S - 2 < nk) __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 3) * LPW));
                 else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
                 wg_barrier();  // stage kt + 1 landed everywhere; stage kt's buffer is free
-    #ifndef TQ_EXP_NOLOAD
                 if (kt + S < nk) issue(kt + S);
-    #endif
                 // past the last stage this reads a stale buffer; the values are unused
                 read_frags(kt + 1, fa[ph ^ 1], fb[ph ^ 1]);
 #pragma unroll
@@ -213,9 +211,7 @@ __global__ __launch_bounds__(128 * WGN) void fp8_gemm_kernel(const uint8_t* __re
             if (kt + S - 2 < nk) __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 3) * LPW));
             else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
             wg_barrier();  // stage kt + 1 landed everywhere; stage kt - 1's buffer is free
-#ifndef TQ_EXP_NOLOAD
             if (kt + S - 1 < nk) issue(kt + S - 1);
-#endif
 #pragma unroll
             for (int jn = 0; jn < TJ; jn++) {
                 if (jn + 1 < TJ) {
