@@ -64,6 +64,51 @@ TQ_DEV void wg_barrier() { asm volatile("s_barrier" ::: "memory"); }
 // s_waitcnt immediate waiting for vmcnt <= n only (gfx9 encoding).
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// Epilogue through LDS: a 32x32 C fragment gives a lane one column
+// (lane & 31) of rows 8 (v / 4) + 4 (lane / 32) + v % 4 (A rows are M, B rows
+// are N).  Each wave scales and converts 32-row bands of its WM x WN tile
+// (rows mw.., columns nw..) into its own LDS region, then writes whole rows
+// with 16-byte stores.  The caller has synchronised the workgroup.
+template <int WM, int WN, int TI, int TJ, int ODT>
+TQ_DEV void fp8_epilogue(uint8_t* sm, const v16f (&acc)[TI][TJ], int mw, int nw, int wave, int lane,
+                         const float* __restrict__ sa, const float* __restrict__ sw,
+                         void* __restrict__ out, int N) {
+    constexpr int OSZ = ODT == TITAN_FP32 ? 4 : 2;
+    constexpr int RB = WN * OSZ + 16;      // LDS bytes per band row (padded)
+    constexpr int PR = WN * OSZ / 16;      // 16-byte pieces per row
+    uint8_t* ep = sm + wave * 32 * RB;
+    float sn[TJ];
+#pragma unroll
+    for (int jn = 0; jn < TJ; jn++) sn[jn] = sw[nw + 32 * jn + (lane & 31)];
+#pragma unroll
+    for (int i = 0; i < TI; i++) {
+        const int mb = mw + 32 * i;  // first row of the band
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int ml = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            const float sm_ = sa[mb + ml];
+#pragma unroll
+            for (int jn = 0; jn < TJ; jn++) {
+                const float val = acc[i][jn][v] * sm_ * sn[jn];
+                uint8_t* dst = ep + ml * RB + (32 * jn + (lane & 31)) * OSZ;
+                if constexpr (ODT == TITAN_FP32) *(float*)dst = val;
+                else if constexpr (ODT == TITAN_FP16) *(uint16_t*)dst = f32_to_f16_rne(val);
+                else *(uint16_t*)dst = f32_to_bf16_rne(val);
+            }
+        }
+        // LDS operations of one wave complete in order: the band is readable
+        const int row = lane >> 1;
+        uint8_t* gout = (uint8_t*)out + ((int64_t)(mb + row) * N + nw) * OSZ;
+#pragma unroll
+        for (int p = 0; p < PR / 2; p++) {
+            const int piece = (lane & 1) * (PR / 2) + p;
+            *(uint4*)(gout + piece * 16) = *(const uint4*)(ep + row * RB + piece * 16);
+        }
+    }
+}
+template <int WN, int ODT>
+constexpr int fp8_epilogue_lds(int nwaves) { return nwaves * 32 * (WN * (ODT == TITAN_FP32 ? 4 : 2) + 16); }
+
 template <int BM, int BN, int WGN, int ODT>
 __global__ __launch_bounds__(128 * WGN) void fp8_gemm_kernel(const uint8_t* __restrict__ A,
                                                           const float* __restrict__ sa,
@@ -229,44 +274,9 @@ __global__ __launch_bounds__(128 * WGN) void fp8_gemm_kernel(const uint8_t* __re
         }
     }
 
-    // Epilogue through LDS: a 32x32 C fragment gives a lane one column
-    // (lane & 31) of rows 8 (v / 4) + 4 (lane / 32) + v % 4 (A rows are M, B
-    // rows are N).  Each wave scales and converts a 32-row band of its tile
-    // into its own LDS region, then writes whole rows with 16-byte stores.
-    constexpr int OSZ = ODT == TITAN_FP32 ? 4 : 2;
-    constexpr int RB = WN * OSZ + 16;      // LDS bytes per band row (padded)
-    constexpr int PR = WN * OSZ / 16;      // 16-byte pieces per row
-    static_assert(NW * 32 * RB <= kF8Stages * (BM + BN) * kF8BK, "epilogue fits in LDS");
+    static_assert(fp8_epilogue_lds<WN, ODT>(NW) <= kF8Stages * (BM + BN) * kF8BK, "epilogue fits in LDS");
     __syncthreads();  // every wave is done with the stage buffers
-    uint8_t* ep = sm + wave * 32 * RB;
-    float sn[TJ];
-#pragma unroll
-    for (int jn = 0; jn < TJ; jn++) sn[jn] = sw[n0 + wn * WN + 32 * jn + (lane & 31)];
-#pragma unroll
-    for (int i = 0; i < TI; i++) {
-        const int mb = m0 + wm * WM + 32 * i;  // first row of the band
-#pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const int ml = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-            const float sm_ = sa[mb + ml];
-#pragma unroll
-            for (int jn = 0; jn < TJ; jn++) {
-                const float val = acc[i][jn][v] * sm_ * sn[jn];
-                uint8_t* dst = ep + ml * RB + (32 * jn + (lane & 31)) * OSZ;
-                if constexpr (ODT == TITAN_FP32) *(float*)dst = val;
-                else if constexpr (ODT == TITAN_FP16) *(uint16_t*)dst = f32_to_f16_rne(val);
-                else *(uint16_t*)dst = f32_to_bf16_rne(val);
-            }
-        }
-        // LDS operations of one wave complete in order: the band is readable
-        const int row = lane >> 1;
-        uint8_t* gout = (uint8_t*)out + ((int64_t)(mb + row) * N + n0 + wn * WN) * OSZ;
-#pragma unroll
-        for (int p = 0; p < PR / 2; p++) {
-            const int piece = (lane & 1) * (PR / 2) + p;
-            *(uint4*)(gout + piece * 16) = *(const uint4*)(ep + row * RB + piece * 16);
-        }
-    }
+    fp8_epilogue<WM, WN, TI, TJ, ODT>(sm, acc, m0 + wm * WM, n0 + wn * WN, wave, lane, sa, sw, out, N);
 }
 
 template <int BM, int BN, int WGN, int ODT>
