@@ -291,9 +291,10 @@ template <int L> using FxFp4 = FxNib<L, true>;
 
 // ============================================================================
 // INT2 affine (dequant.cu:110-172): word (4i+j) = columns 64i + 16j + n of
-// the chunk (code n in bits 2n); groups >= 64 columns.  LDS order per 16
-// columns: [0,8,4,12, 1,9,5,13, 2,10,6,14, 3,11,7,15] -- the field at bits
-// 2k of the two 16-bit halves of (w, w >> 8) are codes (k, k+8) / (k+4, k+12).
+// the chunk (code n in bits 2n); groups >= 64 columns.  The field at bits 2k
+// of the two 16-bit halves holds codes (k, k+8); masked in place (k <= 4) or
+// after one shift by 6 (k = 5..7) it is an exact fp16 subnormal times 4^k (or
+// 4^(k-3)), and the staged activations are divided by the same power of two.
 // ============================================================================
 template <int LAYOUT>
 struct FxInt2 {
@@ -379,16 +380,17 @@ struct FxInt2 {
         for (int i = 0; i < 4; i++) {
             const uint4 xa = *(const uint4*)(xc + 64 * i + 16 * j);
             const uint4 xb = *(const uint4*)(xc + 64 * i + 16 * j + 8);
-            const uint32_t w = r.w[i], u = w >> 8;
-            float s1 = dot2(w & 0x00030003u, xa.x, 0.0f);   // (0, 8)
-            s1 = dot2(u & 0x00030003u, xa.y, s1);           // (4, 12)
-            float s4 = dot2(w & 0x000C000Cu, xa.z, 0.0f);   // (1, 9) x4
-            s4 = dot2(u & 0x000C000Cu, xa.w, s4);           // (5, 13) x4
-            float s16v = dot2(w & 0x00300030u, xb.x, 0.0f); // (2, 10) x16
-            s16v = dot2(u & 0x00300030u, xb.y, s16v);       // (6, 14) x16
-            float s64 = dot2(w & 0x00C000C0u, xb.z, 0.0f);  // (3, 11) x64
-            s64 = dot2(u & 0x00C000C0u, xb.w, s64);         // (7, 15) x64
-            const float v = (__builtin_fmaf(s4, 0.25f, s1) + __builtin_fmaf(s64, 0.25f, s16v) * 0.0625f) * kTwo24;
+            const uint32_t w = r.w[i], u = w >> 6;
+            // fields in place (x 4^k), activations staged / 4^k: one scale
+            float s0 = dot2(w & 0x00030003u, xa.x, 0.0f);  // (0, 8)
+            float s1 = dot2(w & 0x000C000Cu, xa.y, 0.0f);  // (1, 9)
+            s0 = dot2(w & 0x00300030u, xa.z, s0);          // (2, 10)
+            s1 = dot2(w & 0x00C000C0u, xa.w, s1);          // (3, 11)
+            s0 = dot2(w & 0x03000300u, xb.x, s0);          // (4, 12)
+            s1 = dot2(u & 0x00300030u, xb.y, s1);          // (5, 13)
+            s0 = dot2(u & 0x00C000C0u, xb.z, s0);          // (6, 14)
+            s1 = dot2(u & 0x03000300u, xb.w, s1);          // (7, 15)
+            const float v = (s0 + s1) * kTwo24;
             t = __builtin_fmaf(d.s[i], v, t);
         }
         return j == 0 ? t + bias(d, s16) : t;
@@ -397,16 +399,20 @@ struct FxInt2 {
     struct Tmp { f4_t C[4 / GS][NB], O[SX ? 1 : 4 / GS][NB]; };
     template <int NB, int GS, bool SX>
     TQ_DEV static void issue(const Raw& r, int j, const _Float16* const* xt, Tmp<NB, GS, SX>& T) {
-        const h8_t ones = h8_of(make_uint4(kOnes2, kOnes2, kOnes2, kOnes2));
+        // the staged activations are divided by the field weights 4^k: the
+        // ones vectors weigh them back for sum(x)
+        const h8_t ones_a = h8_of(make_uint4(0x3C003C00u, 0x44004400u, 0x4C004C00u, 0x54005400u));
+        const h8_t ones_b = h8_of(make_uint4(0x5C005C00u, 0x4C004C00u, 0x54005400u, 0x5C005C00u));
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int g = i / GS;
-            const uint32_t w = r.w[i];
-            // fields k = 0..3 of w and w >> 8, each shifted down to bit 0
-            const h8_t b0 = h8_of(make_uint4(w & 0x00030003u, (w >> 8) & 0x00030003u,
-                                             (w >> 2) & 0x00030003u, (w >> 10) & 0x00030003u));
-            const h8_t b1 = h8_of(make_uint4((w >> 4) & 0x00030003u, (w >> 12) & 0x00030003u,
-                                             (w >> 6) & 0x00030003u, (w >> 14) & 0x00030003u));
+            const uint32_t w = r.w[i], u = w >> 6;
+            // fields 0..4 of each 16-bit half in place (exact subnormals x 4^k),
+            // fields 5..7 after one shift: 9 operations for 16 codes
+            const h8_t b0 = h8_of(make_uint4(w & 0x00030003u, w & 0x000C000Cu, w & 0x00300030u,
+                                             w & 0x00C000C0u));
+            const h8_t b1 = h8_of(make_uint4(w & 0x03000300u, u & 0x00300030u, u & 0x00C000C0u,
+                                             u & 0x03000300u));
 #pragma unroll
             for (int n = 0; n < NB; n++) {
                 const _Float16* p = xt[n] + 64 * i + 16 * j;
@@ -415,8 +421,8 @@ struct FxInt2 {
                 T.C[g][n] = mfma32(h8_of(xa), b0, first ? f4_zero() : T.C[g][n]);
                 T.C[g][n] = mfma32(h8_of(xb), b1, T.C[g][n]);
                 if constexpr (!SX) {
-                    T.O[g][n] = mfma32(h8_of(xa), ones, first ? f4_zero() : T.O[g][n]);
-                    T.O[g][n] = mfma32(h8_of(xb), ones, T.O[g][n]);
+                    T.O[g][n] = mfma32(h8_of(xa), ones_a, first ? f4_zero() : T.O[g][n]);
+                    T.O[g][n] = mfma32(h8_of(xb), ones_b, T.O[g][n]);
                 }
             }
         }
@@ -440,14 +446,26 @@ struct FxInt2 {
                 }
         }
     }
+    // 16 staged columns: d0 % 16 == 0 gives [0,8,1,9,2,10,3,11] / [1,1,4,4,16,16,64,64],
+    // == 8 gives [4,12,5,13,6,14,7,15] / [256,256,16,16,64,64,256,256] -- the
+    // field weights of the codes they meet (division by a power of two is
+    // exact unless the quotient falls below 2^-14, where it is off by < 2^-25)
     TQ_DEV static uint4 stage8(const _Float16* xr, int d0) {
-        // d0 % 16 == 0: columns [0,8,4,12,1,9,5,13]; == 8: [2,10,6,14,3,11,7,15]
-        const int u = d0 & ~15, k = (d0 & 8) ? 2 : 0;
+        const int u = d0 & ~15;
         _Float16 a[8], b[8], o[8];
         ldh8(xr + u, a);
         ldh8(xr + u + 8, b);
-        o[0] = a[k]; o[1] = b[k]; o[2] = a[k + 4]; o[3] = b[k + 4];
-        o[4] = a[k + 1]; o[5] = b[k + 1]; o[6] = a[k + 5]; o[7] = b[k + 5];
+        if ((d0 & 8) == 0) {
+            o[0] = a[0]; o[1] = b[0];
+            o[2] = a[1] * (_Float16)0.25f; o[3] = b[1] * (_Float16)0.25f;
+            o[4] = a[2] * (_Float16)0.0625f; o[5] = b[2] * (_Float16)0.0625f;
+            o[6] = a[3] * (_Float16)0.015625f; o[7] = b[3] * (_Float16)0.015625f;
+        } else {
+            o[0] = a[4] * (_Float16)0.00390625f; o[1] = b[4] * (_Float16)0.00390625f;
+            o[2] = a[5] * (_Float16)0.0625f; o[3] = b[5] * (_Float16)0.0625f;
+            o[4] = a[6] * (_Float16)0.015625f; o[5] = b[6] * (_Float16)0.015625f;
+            o[6] = a[7] * (_Float16)0.00390625f; o[7] = b[7] * (_Float16)0.00390625f;
+        }
         return pack8(o);
     }
     TQ_DEV static int steps_per_group(const WDesc& w) { return w.g.gs >= 256 ? 4 : w.g.gs / 64; }
