@@ -753,13 +753,24 @@ struct FxQ3K {
     }
     template <int GS>
     TQ_DEV static Dec decode(const WDesc&, const Raw& r, int, int) {
+        // the 16 six-bit scales, four per register as bytes (ggml packing:
+        // low nibbles from bytes 0..7, high 2 bits from bytes 8..11), then
+        // d * (sc - 32) as one fused multiply-add per scale
+        const uint32_t L[4] = {
+            (r.s0 & 0x0F0F0F0Fu) | ((r.s2 & 0x03030303u) << 4),          // k = 0..3
+            (r.s1 & 0x0F0F0F0Fu) | (((r.s2 >> 2) & 0x03030303u) << 4),   // 4..7
+            ((r.s0 >> 4) & 0x0F0F0F0Fu) | (((r.s2 >> 4) & 0x03030303u) << 4),  // 8..11
+            ((r.s1 >> 4) & 0x0F0F0F0Fu) | (((r.s2 >> 6) & 0x03030303u) << 4)}; // 12..15
         Dec o;
-        const float d = f16_to_f32(r.dh);
+        const float d = f16_to_f32(r.dh), d32 = -32.0f * d;
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++)
-                o.dsc[i][jj] = d * (float)q3k_scale(r.s0, r.s1, r.s2, 8 * (i >> 1) + 2 * jj + (i & 1));
+            for (int jj = 0; jj < 4; jj++) {
+                const int k = 8 * (i >> 1) + 2 * jj + (i & 1);
+                const float sc = (float)((L[k >> 2] >> (8 * (k & 3))) & 0xFFu);
+                o.dsc[i][jj] = __builtin_fmaf(sc, d, d32);
+            }
         return o;
     }
     // 3-bit code u = q2 + 4 * hbit of the 4 bytes of word step i at level jj
