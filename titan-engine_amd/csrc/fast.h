@@ -116,7 +116,7 @@ template <int LAYOUT, bool IS_FP4 = false>
 struct FxNib {
     static constexpr int FMT = IS_FP4 ? TITAN_FP4 : TITAN_INT4;
     static constexpr int CHUNK_COLS = 128;
-    static constexpr bool HAS_MFMA = !IS_FP4;
+    static constexpr bool HAS_MFMA = !IS_FP4, PIPE = true;
     struct Off { uint32_t c, s, b; };
     struct Raw { uint32_t w[4], s[4], b[4]; };
     struct Dec { float s[4], b[4]; };
@@ -299,7 +299,7 @@ template <int L> using FxFp4 = FxNib<L, true>;
 template <int LAYOUT>
 struct FxInt2 {
     static constexpr int FMT = TITAN_INT2, CHUNK_COLS = 256;
-    static constexpr bool HAS_MFMA = true;
+    static constexpr bool HAS_MFMA = true, PIPE = true;
     struct Off { uint32_t c, s, b; };
     struct Raw { uint32_t w[4], s[4], b[4]; };
     struct Dec { float s[4], b[4]; };
@@ -480,7 +480,7 @@ struct FxInt2 {
 template <int LAYOUT>
 struct FxNvfp4 {
     static constexpr int FMT = TITAN_NVFP4, CHUNK_COLS = 128;
-    static constexpr bool HAS_MFMA = false;
+    static constexpr bool HAS_MFMA = false, PIPE = true;
     struct Off { uint32_t c, s; };
     struct Raw { uint32_t w[4]; uint32_t s0, s1; };
     struct Dec { float s[4]; };
@@ -570,7 +570,7 @@ struct FxNvfp4 {
 template <int LAYOUT>
 struct FxQ4K {
     static constexpr int FMT = TITAN_Q4_K, CHUNK_COLS = 128;
-    static constexpr bool HAS_MFMA = true;
+    static constexpr bool HAS_MFMA = true, PIPE = true;
     struct Off { uint32_t c, h; };
     struct Raw { uint32_t w[4]; uint4 hdr; };
     struct Dec { float ds[4], dm[4]; };  // [2*c4' + (0: low / 1: high)]
@@ -728,7 +728,10 @@ struct FxQ4K {
 template <int LAYOUT>
 struct FxQ3K {
     static constexpr int FMT = TITAN_Q3_K, CHUNK_COLS = 256;
-    static constexpr bool HAS_MFMA = false;
+    // matrix cores: one 16x16x16 step per (word, level) = one 16-column
+    // sub-block, folded at once with its scale (PIPE = false: issue and
+    // finish of a chunk run back to back)
+    static constexpr bool HAS_MFMA = true, PIPE = false;
     struct Off { uint32_t c, h, s, d; };
     struct Raw { uint32_t w[4]; uint32_t hm0, hm1, s0, s1, s2, dh; };
     struct Dec { float dsc[4][4]; };  // [i][jj]
@@ -824,11 +827,43 @@ struct FxQ3K {
         t *= kTwo24;
         return j == 0 ? t + bias(d, s16) : t;
     }
-    template <int NB, int GS, bool SX> struct Tmp {};
+    template <int NB, int GS, bool SX> struct Tmp { f4_t C[16][NB]; };
     template <int NB, int GS, bool SX>
-    TQ_DEV static void issue(const Raw&, int, const _Float16* const*, Tmp<NB, GS, SX>&) {}
+    TQ_DEV static void issue(const Raw& r, int j, const _Float16* const* xt, Tmp<NB, GS, SX>& T) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                // codes u = q2 + 4 hbit as exact fp16 subnormals, minus 4
+                // (exact): the sub-block's weights are d * sc * b
+                const uint32_t v = code3(r, i, jj);
+                typedef _Float16 q3h2 __attribute__((ext_vector_type(2)));
+                const q3h2 m4 = __builtin_bit_cast(q3h2, 0x80048004u);
+                const q3h2 b01 = __builtin_bit_cast(q3h2, v & 0x00070007u) + m4;
+                const q3h2 b23 = __builtin_bit_cast(q3h2, (v >> 8) & 0x00070007u) + m4;
+                const h4_t b = h4_of(__builtin_bit_cast(uint32_t, b01), __builtin_bit_cast(uint32_t, b23));
+#pragma unroll
+                for (int n = 0; n < NB; n++) {
+                    const _Float16* p = xt[n] + 16 * (8 * (i >> 1) + 4 * (i & 1) + j) + 4 * jj;
+                    const uint2 xv = *(const uint2*)p;
+                    T.C[4 * i + jj][n] = mfma16(h4_of(xv.x, xv.y), b, f4_zero());
+                }
+            }
+    }
     template <int NB, int NV, int GS, bool SX>
-    TQ_DEV static void finish(const Tmp<NB, GS, SX>&, const Dec&, const float*, f4_t*) {}
+    TQ_DEV static void finish(const Tmp<NB, GS, SX>& T, const Dec& d, const float*, f4_t* acc) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const float sc = d.dsc[i][jj] * kTwo24;
+#pragma unroll
+                for (int n = 0; n < NB; n++)
+#pragma unroll
+                    for (int v = 0; v < NV; v++)
+                        acc[n][v] = __builtin_fmaf(sc, T.C[4 * i + jj][n][v], acc[n][v]);
+            }
+    }
     TQ_DEV static uint4 stage8(const _Float16* xr, int d0) {
         // d0 = 16 * (8h + l4) + 8 * p: levels jj = 2p, 2p+1 of positions l..l+3
         const int e = d0 >> 4, h = e >> 3, l = (e & 7) * 4, jj = (d0 & 8) ? 2 : 0;
@@ -850,7 +885,7 @@ struct FxQ3K {
 template <int LAYOUT>
 struct FxFp8 {
     static constexpr int FMT = TITAN_FP8_E4M3, CHUNK_COLS = 64;
-    static constexpr bool HAS_MFMA = false;
+    static constexpr bool HAS_MFMA = false, PIPE = true;
     struct Off { uint32_t c; };
     struct Raw { uint32_t w[4]; };
     struct Dec {};

@@ -161,6 +161,7 @@ int run_gemv(const titan_qweight* Ws, const void* const* Xs, const int64_t* ldx,
         case TITAN_INT4: has_mfma = gemv_has_mfma_int4(); break;
         case TITAN_INT2: has_mfma = gemv_has_mfma_int2(); break;
         case TITAN_Q4_K: has_mfma = gemv_has_mfma_q4k(); break;
+        case TITAN_Q3_K: has_mfma = gemv_has_mfma_q3k(); break;
         default: break;
     }
     // one group size per launch (the kernels take the word steps per group

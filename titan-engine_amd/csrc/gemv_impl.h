@@ -232,6 +232,21 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
                 const int tok = 16 * n + r;
                 xt[n] = xh + (tok < M ? tok : 0) * pc;
             }
+            if constexpr (!F::PIPE) {
+                typename F::template Tmp<NB, GS, SX> T1;
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const int cc = chunk_at(ph, g, u);
+                    if (cc >= nchunks) continue;  // uniform per wave
+                    const int lbase = (cc - ph * pchunks) * F::CHUNK_COLS;
+                    const _Float16* xu[NB];
+#pragma unroll
+                    for (int n = 0; n < NB; n++) xu[n] = xt[n] + lbase;
+                    F::template issue<NB, GS, SX>(R[u], j, xu, T1);
+                    const typename F::Dec dec = F::template decode<GS>(W, R[u], cc, j);
+                    F::template finish<NB, NV, GS, SX>(T1, dec, s16 + 4 * (lbase >> 5), macc);
+                }
+            } else {
             typename F::template Tmp<NB, GS, SX> T[2];
 #pragma unroll
             for (int u = 0; u <= U; u++) {
@@ -253,6 +268,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
                         F::template finish<NB, NV, GS, SX>(T[(u - 1) & 1], dec, s16 + 4 * (lbase >> 5), macc);
                     }
                 }
+            }
             }
         } else {
 #pragma unroll
