@@ -781,6 +781,14 @@ struct FxQ3K {
         const uint32_t hm = (i & 1) ? r.hm1 : r.hm0;
         return ((r.w[i] >> (2 * jj)) & 0x03030303u) | (((hm >> (4 * (i >> 1) + jj)) & 0x01010101u) << 2);
     }
+    // the same codes in bits 0..2 of each byte, bits 3..7 undefined: two
+    // shifts and one bit-field insert
+    TQ_DEV static uint32_t code3x(const Raw& r, int i, int jj) {
+        const uint32_t hm = (i & 1) ? r.hm1 : r.hm0;
+        const int sh = 4 * (i >> 1) + jj - 2;  // hmask bit -> bit 2 of the byte
+        const uint32_t y = sh >= 0 ? hm >> sh : hm << -sh;
+        return ((r.w[i] >> (2 * jj)) & 0x03030303u) | (y & ~0x03030303u);
+    }
     TQ_DEV static float bias(const Dec& d, const float* s16) {
         // value = d*sc*(u - 4): the -4 term is -4 d sc sum(x) per sub-block
         float t = 0.0f;
@@ -836,7 +844,7 @@ struct FxQ3K {
             for (int jj = 0; jj < 4; jj++) {
                 // codes u = q2 + 4 hbit as exact fp16 subnormals, minus 4
                 // (exact): the sub-block's weights are d * sc * b
-                const uint32_t v = code3(r, i, jj);
+                const uint32_t v = code3x(r, i, jj);
                 typedef _Float16 q3h2 __attribute__((ext_vector_type(2)));
                 const q3h2 m4 = __builtin_bit_cast(q3h2, 0x80048004u);
                 const q3h2 b01 = __builtin_bit_cast(q3h2, v & 0x00070007u) + m4;
