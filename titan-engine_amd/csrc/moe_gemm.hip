@@ -229,6 +229,18 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemm_kernel(MoeGemmArgs a) {
     }
 }
 
+// bf16 / fp32 activations -> fp16 once, 8 elements per thread (every
+// workgroup of every selected expert stages these rows again).
+template <int XDT>
+__global__ __launch_bounds__(256) void to_f16_kernel(const void* __restrict__ x, int64_t n8,
+                                                     _Float16* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n8) return;
+    XItem<XDT> v;
+    v.load(x, i * 8);
+    *(uint4*)(out + i * 8) = v.h();
+}
+
 // Counting sort of the (token, slot) pairs by expert.  One workgroup; the
 // order of pairs inside an expert is irrelevant to the results (each token is
 // its own row of the GEMMs and the combine reads positions through `inv`).
@@ -315,6 +327,7 @@ struct MoeWs {
     int* inv;
     _Float16* act;
     float* y;
+    _Float16* xh;  // the tokens' activations as fp16 (bf16 / fp32 input)
     size_t bytes;
 };
 
@@ -326,13 +339,15 @@ MoeWs carve(void* base, int tokens, int k, int E, int hidden, int inter) {
     size_t o = 0;
     auto take = [&](size_t n) { size_t at = o; o = align256(o + n); return at; };
     const size_t o_off = take((size_t)(E + 1) * 4), o_pair = take(P * 4), o_inv = take(P * 4),
-                 o_act = take(P * inter * 2), o_y = take(P * hidden * 4);
+                 o_act = take(P * inter * 2), o_y = take(P * hidden * 4),
+                 o_xh = take((size_t)tokens * hidden * 2);
     char* b = (char*)base;
     w.off = (int*)(b + o_off);
     w.pair_at = (int*)(b + o_pair);
     w.inv = (int*)(b + o_inv);
     w.act = (_Float16*)(b + o_act);
     w.y = (float*)(b + o_y);
+    w.xh = (_Float16*)(b + o_xh);
     w.bytes = o;
     return w;
 }
@@ -341,17 +356,10 @@ template <int TM, int SL, int RT, bool GATED>
 int launch_moe(const MoeGemmArgs& a, int x_dtype, int E, hipStream_t st) {
     if (a.N % (kMoeRowsPerWg * RT)) return TITAN_ERR_UNSUPPORTED;
     dim3 grid(a.N / (kMoeRowsPerWg * RT), E);
-    switch (x_dtype) {
-        case TITAN_FP16:
-            hipLaunchKernelGGL((moe_gemm_kernel<TM, SL, RT, GATED, TITAN_FP16>), grid, dim3(kMoeThreads), 0, st, a);
-            break;
-        case TITAN_BF16:
-            hipLaunchKernelGGL((moe_gemm_kernel<TM, SL, RT, GATED, TITAN_BF16>), grid, dim3(kMoeThreads), 0, st, a);
-            break;
-        default:
-            hipLaunchKernelGGL((moe_gemm_kernel<TM, SL, RT, GATED, TITAN_FP32>), grid, dim3(kMoeThreads), 0, st, a);
-            break;
-    }
+    // Activations always arrive as fp16: the forward converts other types once.
+    if (x_dtype != TITAN_FP16) return TITAN_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL((moe_gemm_kernel<TM, SL, RT, GATED, TITAN_FP16>), grid, dim3(kMoeThreads), 0,
+                       st, a);
     return tqh::launch_status();
 }
 
@@ -438,6 +446,18 @@ extern "C" int titan_moe_nvfp4_forward(const titan_nvfp4_expert* experts, int nu
     MoeGemmArgs g{};
     g.experts = experts;
     g.x = x;
+    int gx_dtype = x_dtype;
+    if (x_dtype != TITAN_FP16) {
+        const int64_t n8 = (int64_t)tokens * hidden / 8;
+        const dim3 grid((unsigned)((n8 + 255) / 256));
+        if (x_dtype == TITAN_BF16)
+            hipLaunchKernelGGL(to_f16_kernel<TITAN_BF16>, grid, dim3(256), 0, stream, x, n8, ws.xh);
+        else
+            hipLaunchKernelGGL(to_f16_kernel<TITAN_FP32>, grid, dim3(256), 0, stream, x, n8, ws.xh);
+        if (int st = tqh::launch_status()) return st;
+        g.x = ws.xh;
+        gx_dtype = TITAN_FP16;
+    }
     g.ldx = hidden;
     g.pair_at = ws.pair_at;
     g.k = k;
@@ -446,7 +466,7 @@ extern "C" int titan_moe_nvfp4_forward(const titan_nvfp4_expert* experts, int nu
     g.K = hidden;
     g.out = ws.act;
     g.ldo = inter;
-    if (int st = launch_moe_tm<true>(tm, g, x_dtype, num_experts, stream)) return st;
+    if (int st = launch_moe_tm<true>(tm, g, gx_dtype, num_experts, stream)) return st;
 
     MoeGemmArgs d{};
     d.experts = experts;
