@@ -117,8 +117,10 @@ struct FxNib {
     static constexpr int FMT = IS_FP4 ? TITAN_FP4 : TITAN_INT4;
     static constexpr int CHUNK_COLS = 128;
     static constexpr bool HAS_MFMA = !IS_FP4, PIPE = true;
+    // tiled INT4: the scales come in 16-byte cells, one load per GS chunks
+    static constexpr bool SB_CELL = LAYOUT == TITAN_LAYOUT_TILED && !IS_FP4;
     struct Off { uint32_t c, s, b; };
-    struct Raw { uint32_t w[4], s[4], b[4]; };
+    struct Raw { uint32_t w[4], s[4], b[4]; uint4 q; };
     struct Dec { float s[4], b[4]; };
     TQ_DEV static Off base(const WDesc& w, int row, int j) {
         const Geo& g = w.g;
@@ -139,6 +141,7 @@ struct FxNib {
             uint4 q = ld_u128(w.codes + (o.c + (uint32_t)c * 1024u));
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
+        if constexpr (SB_CELL) return;  // load_cell
 #pragma unroll
         for (int i = GS - 1; i < 4; i += GS) {  // last word step of each group
             const uint32_t grp = (uint32_t)group_of(w, c * 128 + 32 * i);
@@ -165,6 +168,26 @@ struct FxNib {
                 d.s[i] = f16_to_f32(r.s[k]);
                 d.b[i] = IS_FP4 ? 0.0f : f16_to_f32(r.b[k]);
             }
+        }
+        return d;
+    }
+    // Scale cells (tiled INT4 / INT2): chunk c's groups sit in cell c / GS at
+    // entries (c % GS) * (4 / GS) + (step / GS); the cell is loaded with the
+    // first chunk of its GS chunks (the caller's chunk groups start at
+    // multiples of 4).
+    template <int GS>
+    TQ_DEV static void load_cell(const WDesc& w, const Off& o, int c, Raw& r) {
+        r.q = ld_u128(w.codes + (o.s + (uint32_t)(c / GS) * 256u));
+    }
+    template <int GS>
+    TQ_DEV static Dec decode_cell(const uint4& q, int u) {
+        const uint32_t e[4] = {q.x, q.y, q.z, q.w};
+        Dec d;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t v = e[(u % GS) * (4 / GS) + i / GS];
+            d.s[i] = f16_to_f32(v & 0xFFFF);
+            d.b[i] = f16_to_f32(v >> 16);
         }
         return d;
     }
@@ -300,8 +323,9 @@ template <int LAYOUT>
 struct FxInt2 {
     static constexpr int FMT = TITAN_INT2, CHUNK_COLS = 256;
     static constexpr bool HAS_MFMA = true, PIPE = true;
+    static constexpr bool SB_CELL = LAYOUT == TITAN_LAYOUT_TILED;
     struct Off { uint32_t c, s, b; };
-    struct Raw { uint32_t w[4], s[4], b[4]; };
+    struct Raw { uint32_t w[4], s[4], b[4]; uint4 q; };
     struct Dec { float s[4], b[4]; };
     TQ_DEV static Off base(const WDesc& w, int row, int j) {
         const Geo& g = w.g;
@@ -320,6 +344,7 @@ struct FxInt2 {
             uint4 q = ld_u128(w.codes + (o.c + (uint32_t)c * 1024u));
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
+        if constexpr (SB_CELL) return;  // load_cell
 #pragma unroll
         for (int i = GS - 1; i < 4; i += GS) {  // last word step of each group
             const uint32_t grp = (uint32_t)group_of(w, c * 256 + 64 * i);
@@ -344,6 +369,26 @@ struct FxInt2 {
                 d.s[i] = f16_to_f32(r.s[k]);
                 d.b[i] = f16_to_f32(r.b[k]);
             }
+        }
+        return d;
+    }
+    // Scale cells (tiled INT4 / INT2): chunk c's groups sit in cell c / GS at
+    // entries (c % GS) * (4 / GS) + (step / GS); the cell is loaded with the
+    // first chunk of its GS chunks (the caller's chunk groups start at
+    // multiples of 4).
+    template <int GS>
+    TQ_DEV static void load_cell(const WDesc& w, const Off& o, int c, Raw& r) {
+        r.q = ld_u128(w.codes + (o.s + (uint32_t)(c / GS) * 256u));
+    }
+    template <int GS>
+    TQ_DEV static Dec decode_cell(const uint4& q, int u) {
+        const uint32_t e[4] = {q.x, q.y, q.z, q.w};
+        Dec d;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t v = e[(u % GS) * (4 / GS) + i / GS];
+            d.s[i] = f16_to_f32(v & 0xFFFF);
+            d.b[i] = f16_to_f32(v >> 16);
         }
         return d;
     }

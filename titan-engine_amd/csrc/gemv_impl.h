@@ -17,8 +17,14 @@
 //    waves through LDS; MFMA accumulators already hold whole-row sums.
 #pragma once
 #include "fast.h"
+#include <type_traits>
 
 namespace tq {
+
+template <class F, class = void>
+struct requires_sb_cell : std::false_type {};
+template <class F>
+struct requires_sb_cell<F, std::void_t<decltype(F::SB_CELL)>> : std::true_type {};
 
 #ifndef TQ_GEMV_U
 #define TQ_GEMV_U 4
@@ -149,6 +155,24 @@ TQ_DEV void stage_f16(_Float16* xh, float* s16, int pc, const void* x, int64_t l
 template <class F, int M, int MODE>
 constexpr int gemv_u() { return TQ_GEMV_U; }
 
+// Formats whose tiled scales come in 16-byte cells (SB_CELL) decode chunk u
+// of a group from the cell loaded with chunk u - u % GS.
+template <class F>
+constexpr bool has_sb_cell() {
+    if constexpr (requires_sb_cell<F>::value) return F::SB_CELL;
+    else return false;
+}
+template <class F, int GS, class RawArr>
+TQ_DEV typename F::Dec decode_u(const WDesc& W, const RawArr& R, int u, int cc, int j) {
+    if constexpr (has_sb_cell<F>()) return F::template decode_cell<GS>(R[u - u % GS].q, u);
+    else return F::template decode<GS>(W, R[u], cc, j);
+}
+
+#ifdef TQ_GEMV_TRACE
+// diagnostic build only: per-wave timestamps (100 MHz) and hardware ids
+static __device__ unsigned long long tq_gemv_trace[16384 * 4];
+#endif
+
 template <class F, int M, int MODE, int GS = 4>
 __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -201,12 +225,23 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     // group q = ph * gpp + g: chunks ph * pchunks + (g * U + u) * KS + part.
     // Groups are visited in order; the phase of a group is tracked
     // incrementally (no division per chunk).
-    auto chunk_at = [&](int ph, int g, int u) { return ph * pchunks + ((g * U + u) << ks_log) + part; };
+    // Each of the KS waves takes a contiguous quarter (half) of the phase, so
+    // a group is U consecutive chunks starting at a multiple of U.
+    const int pspan = pchunks >> ks_log;
+    auto chunk_at = [&](int ph, int g, int u) { return ph * pchunks + part * pspan + g * U + u; };
     auto load_group = [&](int ph, int g, typename F::Raw (&R)[U]) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int cc = chunk_at(ph, g, u);
             F::template load<GS>(W, off, cc < nchunks ? cc : 0, j, R[u]);
+        }
+        if constexpr (has_sb_cell<F>()) {
+            static_assert(U % GS == 0, "a chunk group holds whole scale cells");
+#pragma unroll
+            for (int u = 0; u < U; u += GS) {
+                const int cc = chunk_at(ph, g, u);
+                F::template load_cell<GS>(W, off, cc < nchunks ? cc : 0, R[u]);
+            }
         }
     };
     auto fold_group = [&](int ph, int g, const typename F::Raw (&R)[U]) {
@@ -232,19 +267,33 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
                 const int tok = 16 * n + r;
                 xt[n] = xh + (tok < M ? tok : 0) * pc;
             }
+            // Branch-free over the group (a branch per chunk would leave the
+            // compiler unsure which loads have landed, and it would then drain
+            // the next group's loads too): chunks past the end of the row fold
+            // the staged columns of chunk 0 and are discarded by a select.
+            auto lbase_of = [&](int cc) { return cc < nchunks ? (cc - ph * pchunks) * F::CHUNK_COLS : 0; };
+            auto fold_into = [&](const typename F::template Tmp<NB, GS, SX>& T, const typename F::Dec& dec,
+                                 int cc, int lbase) {
+                f4_t m2[NB];
+#pragma unroll
+                for (int n = 0; n < NB; n++) m2[n] = macc[n];
+                F::template finish<NB, NV, GS, SX>(T, dec, s16 + 4 * (lbase >> 5), m2);
+                const bool live = cc < nchunks;
+#pragma unroll
+                for (int n = 0; n < NB; n++) macc[n] = live ? m2[n] : macc[n];
+            };
             if constexpr (!F::PIPE) {
                 typename F::template Tmp<NB, GS, SX> T1;
 #pragma unroll
                 for (int u = 0; u < U; u++) {
                     const int cc = chunk_at(ph, g, u);
-                    if (cc >= nchunks) continue;  // uniform per wave
-                    const int lbase = (cc - ph * pchunks) * F::CHUNK_COLS;
+                    const int lbase = lbase_of(cc);
                     const _Float16* xu[NB];
 #pragma unroll
                     for (int n = 0; n < NB; n++) xu[n] = xt[n] + lbase;
                     F::template issue<NB, GS, SX>(R[u], j, xu, T1);
-                    const typename F::Dec dec = F::template decode<GS>(W, R[u], cc, j);
-                    F::template finish<NB, NV, GS, SX>(T1, dec, s16 + 4 * (lbase >> 5), macc);
+                    const typename F::Dec dec = decode_u<F, GS>(W, R, u, cc, j);
+                    fold_into(T1, dec, cc, lbase);
                 }
             } else {
             typename F::template Tmp<NB, GS, SX> T[2];
@@ -252,21 +301,16 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             for (int u = 0; u <= U; u++) {
                 if (u < U) {
                     const int cc = chunk_at(ph, g, u);
-                    if (cc < nchunks) {
-                        const int lbase = (cc - ph * pchunks) * F::CHUNK_COLS;
-                        const _Float16* xu[NB];
+                    const int lbase = lbase_of(cc);
+                    const _Float16* xu[NB];
 #pragma unroll
-                        for (int n = 0; n < NB; n++) xu[n] = xt[n] + lbase;
-                        F::template issue<NB, GS, SX>(R[u], j, xu, T[u & 1]);
-                    }
+                    for (int n = 0; n < NB; n++) xu[n] = xt[n] + lbase;
+                    F::template issue<NB, GS, SX>(R[u], j, xu, T[u & 1]);
                 }
                 if (u > 0) {
                     const int cp = chunk_at(ph, g, u - 1);
-                    if (cp < nchunks) {
-                        const int lbase = (cp - ph * pchunks) * F::CHUNK_COLS;
-                        const typename F::Dec dec = F::template decode<GS>(W, R[u - 1], cp, j);
-                        F::template finish<NB, NV, GS, SX>(T[(u - 1) & 1], dec, s16 + 4 * (lbase >> 5), macc);
-                    }
+                    const typename F::Dec dec = decode_u<F, GS>(W, R, u - 1, cp, j);
+                    fold_into(T[(u - 1) & 1], dec, cp, lbase_of(cp));
                 }
             }
             }
@@ -276,7 +320,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
                 const int cc = chunk_at(ph, g, u);
                 if (cc >= nchunks) continue;  // uniform per wave
                 const int lbase = (cc - ph * pchunks) * F::CHUNK_COLS;
-                const typename F::Dec dec = F::template decode<GS>(W, R[u], cc, j);
+                const typename F::Dec dec = decode_u<F, GS>(W, R, u, cc, j);
 #pragma unroll
                 for (int m = 0; m < M; m++) {
                     if constexpr (MODE == kModeF32)
@@ -296,21 +340,31 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     auto advance = [&](int& p, int& q) {
         if (++q == gpp) { q = 0; ++p; }
     };
+#ifdef TQ_GEMV_TRACE
+    const unsigned long long tr0 = __builtin_amdgcn_s_memrealtime();
+#endif
     load_group(0, 0, ra);
     for (int n = 0; n < ngroups; n += 2) {
         int ph1 = ph, g1 = g;
         advance(ph1, g1);
-        if (n + 1 < ngroups) load_group(ph1, g1, rb);
+        // past the last group the loads repeat the previous group (cache
+        // hits): unconditional loads keep the waits exact
+        const bool has1 = n + 1 < ngroups;
+        load_group(has1 ? ph1 : ph, has1 ? g1 : g, rb);
         fold_group(ph, g, ra);
-        if (n + 1 >= ngroups) break;
+        if (!has1) break;
         int ph2 = ph1, g2 = g1;
         advance(ph2, g2);
-        if (n + 2 < ngroups) load_group(ph2, g2, ra);
+        const bool has2 = n + 2 < ngroups;
+        load_group(has2 ? ph2 : ph1, has2 ? g2 : g1, ra);
         fold_group(ph1, g1, rb);
         ph = ph2;
         g = g2;
     }
 
+#ifdef TQ_GEMV_TRACE
+    const unsigned long long tr1 = __builtin_amdgcn_s_memrealtime();
+#endif
     // per-lane results: MFMA lane (r, q = j) holds tokens 16n + 4j + v of row
     // r; VALU lanes hold partial sums of row r over their words.
     float res[M];
@@ -360,6 +414,21 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             }
         }
     }
+#ifdef TQ_GEMV_TRACE
+    {
+        unsigned hw, xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        const int wid = blockIdx.x * kGemvWaves + wave;
+        if (lane == 0 && wid < 16384) {
+            unsigned long long* t = tq_gemv_trace + 4 * wid;
+            t[0] = tr0;
+            t[1] = tr1;
+            t[2] = __builtin_amdgcn_s_memrealtime();
+            t[3] = ((unsigned long long)(pi | (part << 8) | ((xcc & 15) << 16)) << 32) | hw;
+        }
+    }
+#endif
 }
 
 // ---- generic fallback for shapes the fast kernel does not take ------------------

@@ -3,7 +3,9 @@
 // Shared by the host repack (repack.cpp) and the device kernels so that the
 // two can never disagree about where a byte lives.
 //
-// TILED layout (one buffer, all planes back to back, same byte count as REF):
+// TILED layout (one buffer, all planes back to back; the same byte count as
+// REF except for INT4 / INT2 scale slots, padded to whole 16-byte cells and
+// repeated for groups longer than one chunk):
 //   code plane   row r's code bytes (K-quants: the concatenated qs arrays of
 //                its blocks) cut into 64-byte chunks of 16 words; tile t = rows
 //                16t..16t+15; chunk c of tile t is 1 KiB at
@@ -81,10 +83,25 @@ TQ_HD size_t tiled_code_byte(const Geo& g, int row, int b) {
 }
 
 // ---- TILED aux planes (offsets from the start of the buffer) ----------------
-// INT4 / INT2: u32 (scale | bias << 16) at [t][group][r].
-TQ_HD size_t tiled_sb_off(const Geo& g, int row, int grp) {
+// INT4 / INT2: u32 words (scale | bias << 16) in "slots", four slots of one
+// row in one 16-byte cell at [t][slot / 4][r][slot % 4], so that a lane reads
+// the scales of four chunks (groups of at least one chunk) or of one chunk
+// (smaller groups) with a single 16-byte load.  Groups of at least one chunk
+// have one slot per chunk (slot c = the group of chunk c; a group of n chunks
+// is stored n times); smaller groups have one slot per group.
+TQ_HD int tiled_sb_slots(const Geo& g) { return g.gs >= g.chunk_cols ? g.nchunks : g.ngroups; }
+TQ_HD int tiled_sb_cells(const Geo& g) { return (tiled_sb_slots(g) + 3) >> 2; }
+TQ_HD size_t tiled_sb_slot_off(const Geo& g, int row, int slot) {
     return tiled_code_plane_bytes(g) +
-           (((size_t)(row >> 4) * g.ngroups + grp) * 16 + (row & 15)) * 4;
+           ((((size_t)(row >> 4) * tiled_sb_cells(g) + (slot >> 2)) * 16 + (row & 15)) * 4 + (slot & 3)) * 4;
+}
+// first slot holding group grp, and how many slots hold it
+TQ_HD int tiled_sb_slot_of(const Geo& g, int grp) {
+    return g.gs >= g.chunk_cols ? grp * (g.gs / g.chunk_cols) : grp;
+}
+TQ_HD int tiled_sb_copies(const Geo& g) { return g.gs >= g.chunk_cols ? g.gs / g.chunk_cols : 1; }
+TQ_HD size_t tiled_sb_off(const Geo& g, int row, int grp) {
+    return tiled_sb_slot_off(g, row, tiled_sb_slot_of(g, grp));
 }
 // FP4: u16 scale at [t][group][r].
 TQ_HD size_t tiled_fp4s_off(const Geo& g, int row, int grp) {
@@ -131,7 +148,7 @@ TQ_HD size_t tiled_total_bytes(int fmt, int rows, int cols, int gs) {
     switch (fmt) {
         case TITAN_INT4:
         case TITAN_INT2:
-            if (gs_ok) total = codes + (size_t)rows * g.ngroups * 4;
+            if (gs_ok) total = codes + (size_t)rows * tiled_sb_cells(g) * 16;
             break;
         case TITAN_FP4:
             if (gs_ok) total = codes + (size_t)rows * g.ngroups * 2;

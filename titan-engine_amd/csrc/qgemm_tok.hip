@@ -120,8 +120,10 @@ __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) 
             w.c[q] = *(const uint4*)(P.w + code_off[q] + (uint32_t)s * 1024u);
 #pragma unroll
             for (int f = 0; f < NF; f++) {
+                // scale slot: one per chunk for groups of a chunk or more, else one per group
                 const uint32_t g = (uint32_t)((s * kTokSlab + f * FW * 32) >> gshift);
-                w.sb[q][f] = *(const uint32_t*)(P.w + sb_base[q] + g * 64u);
+                const uint32_t sl = P.gs >= kTokSlab ? (uint32_t)s : g;
+                w.sb[q][f] = *(const uint32_t*)(P.w + sb_base[q] + (sl >> 2) * 256u + (sl & 3u) * 4u);
             }
         }
     };

@@ -59,6 +59,7 @@ extern "C" int titan_repack_host(int fmt, int rows, int cols, int gs, const void
 
     Geo g = tq::make_geo(fmt, rows, cols, gs);
     uint8_t* out = (uint8_t*)tiled;
+    memset(out, 0, need);  // padding slots read as zero
     RefRowCodes rc(g, codes);
     for (int r = 0; r < rows; r++) {
         const uint8_t* src = rc.row(r);
@@ -76,7 +77,8 @@ extern "C" int titan_repack_host(int fmt, int rows, int cols, int gs, const void
                 for (int q = 0; q < g.ngroups; q++) {
                     uint32_t v = (uint32_t)s16[(size_t)r * g.ngroups + q] |
                                  ((uint32_t)b16[(size_t)r * g.ngroups + q] << 16);
-                    memcpy(out + tq::tiled_sb_off(g, r, q), &v, 4);
+                    const int s0 = tq::tiled_sb_slot_of(g, q), n = tq::tiled_sb_copies(g);
+                    for (int k = 0; k < n; k++) memcpy(out + tq::tiled_sb_slot_off(g, r, s0 + k), &v, 4);
                 }
                 break;
             case TITAN_FP4:
