@@ -297,9 +297,13 @@ struct FxNib {
     // INT4 (matrix cores): the odd columns are pre-divided by 16 to meet their
     // codes, which enter 16x too large (exact for |x| >= 2^-10; below that the
     // quotient is an fp16 subnormal, off by at most 2^-25)
-    TQ_DEV static uint4 stage8(const _Float16* xr, int d0) {
+    static constexpr bool STAGE_LOCAL = true;  // stage8 reads only columns d0..d0+7
+    TQ_DEV static uint4 stage8(const _Float16* xr, int d0) { return stage8_raw(*(const uint4*)(xr + d0)); }
+    TQ_DEV static uint4 stage8_raw(uint4 raw) {
         _Float16 h[8], o[8];
-        ldh8(xr + d0, h);
+        const h8_t t = h8_of(raw);
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = t[i];
         const _Float16 k = IS_FP4 ? (_Float16)1.0f : (_Float16)0.0625f;
         o[0] = h[0]; o[1] = h[4]; o[2] = h[2]; o[3] = h[6];
         o[4] = h[1] * k; o[5] = h[5] * k; o[6] = h[3] * k; o[7] = h[7] * k;

@@ -22,6 +22,10 @@
 namespace tq {
 
 template <class F, class = void>
+struct has_stage_local : std::false_type {};
+template <class F>
+struct has_stage_local<F, std::void_t<decltype(F::STAGE_LOCAL)>> : std::true_type {};
+template <class F, class = void>
 struct requires_sb_cell : std::false_type {};
 template <class F>
 struct requires_sb_cell<F, std::void_t<decltype(F::SB_CELL)>> : std::true_type {};
@@ -36,6 +40,9 @@ constexpr int kGemvThreads = kGemvWaves * kWave;
 #endif
 #ifndef TQ_GEMV_WAVES_TARGET
 #define TQ_GEMV_WAVES_TARGET 2048
+#endif
+#ifndef TQ_GEMV_DEPTH
+#define TQ_GEMV_DEPTH 2  // weight groups in flight + 1
 #endif
 #ifndef TQ_GEMV_KS_MAX
 #define TQ_GEMV_KS_MAX 2
@@ -168,6 +175,22 @@ TQ_DEV typename F::Dec decode_u(const WDesc& W, const RawArr& R, int u, int cc, 
     else return F::template decode<GS>(W, R[u], cc, j);
 }
 
+// Formats whose stage8 permutes only its own 8 columns (STAGE_LOCAL) stage
+// in one round of 16-byte loads per thread, issued before the first weights.
+template <class F>
+constexpr bool stage_local() {
+    if constexpr (has_stage_local<F>::value) return F::STAGE_LOCAL;
+    else return false;
+}
+constexpr int kStageItems = 8;
+template <int NI>
+struct XStage { uint4 v[NI]; unsigned live; };
+template <class F>
+TQ_DEV uint4 stage8_raw_of(uint4 v) {
+    if constexpr (stage_local<F>()) return F::stage8_raw(v);
+    else return v;
+}  // 16-byte activation loads per thread and round
+
 #ifdef TQ_GEMV_TRACE
 // diagnostic build only: per-wave timestamps (100 MHz) and hardware ids
 static __device__ unsigned long long tq_gemv_trace[16384 * 4];
@@ -233,7 +256,11 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int cc = chunk_at(ph, g, u);
+#ifdef TQ_GEMV_NOLOAD
+            F::template load<GS>(W, off, 0, j, R[u]);
+#else
             F::template load<GS>(W, off, cc < nchunks ? cc : 0, j, R[u]);
+#endif
         }
         if constexpr (has_sb_cell<F>()) {
             static_assert(U % GS == 0, "a chunk group holds whole scale cells");
@@ -244,8 +271,82 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             }
         }
     };
+    // One-round staging (STAGE_LOCAL formats, fp16 activations): item e of a
+    // phase is token e / nb8, columns [8 (e % nb8), +8); every load of a round
+    // is issued before any is used, and the column sums come from the same
+    // registers (a shuffle over the lanes of one sum window).
+    constexpr bool LOCAL = stage_local<F>() && MODE != kModeF32;
+    auto phase_cols = [&](int ph, int& col0, int& ncols) {
+        col0 = ph * pchunks * F::CHUNK_COLS;
+        ncols = min(pchunks * F::CHUNK_COLS, W.g.cols - col0);
+    };
+    auto stage_issue = [&](int ph, int round, auto& S) {
+        constexpr int NI = sizeof(S.v) / sizeof(uint4);
+        int col0, ncols;
+        phase_cols(ph, col0, ncols);
+        const int nb8 = ncols >> 3;
+        const _Float16* xb = (const _Float16*)P.x;
+        S.live = 0;
+#pragma unroll
+        for (int k = 0; k < NI; k++) {
+            const int e = round + k * kGemvThreads + tid;
+            const int m = e / nb8, d = e - m * nb8;
+            const bool live = m < M && m < a.mcount;
+            const int64_t src = live ? (int64_t)(a.m0 + m) * P.ldx + col0 + 8 * d : (int64_t)a.m0 * P.ldx + col0;
+            S.v[k] = *(const uint4*)(xb + src);
+            S.live |= live ? 1u << k : 0u;
+        }
+    };
+    auto stage_commit = [&](int ph, int round, const auto& S) {
+        constexpr int NI = sizeof(S.v) / sizeof(uint4);
+        int col0, ncols;
+        phase_cols(ph, col0, ncols);
+        const int nb8 = ncols >> 3;
+#pragma unroll
+        for (int k = 0; k < NI; k++) {
+            const int e = round + k * kGemvThreads + tid;
+            const int m = e / nb8, d = e - m * nb8;
+            const uint4 v = (S.live >> k) & 1u ? S.v[k] : make_uint4(0, 0, 0, 0);
+            if (m < M) *(uint4*)(xh + m * pc + 8 * d) = stage8_raw_of<F>(v);
+            if constexpr (SX || MODE == kModeDot2) {
+                // SX: sums over one scale window at s16[4 * (col / 32) + token];
+                // VALU fold: sums over 16 columns at s16[token * (pc / 16) + col / 16]
+                constexpr int SW = SX ? F::template sx_cols<GS>() : 16, WL = SW / 8;
+                const h8_t h = h8_of(v);
+                float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; i += 2) {
+                    a0 += (float)h[i];
+                    a1 += (float)h[i + 1];
+                }
+                float sum = a0 + a1;
+#pragma unroll
+                for (int o = 1; o < WL; o <<= 1) sum += __shfl_xor(sum, o, kWave);
+                if (m < M && d % WL == 0) {
+                    if constexpr (SX) s16[4 * ((8 * d / SW) * (SW / 32)) + m] = sum;
+                    else s16[m * (pc >> 4) + d / 2] = sum;
+                }
+            }
+        }
+    };
+    auto stage_all = [&](int ph) {  // later phases: one round after another
+        int col0, ncols;
+        phase_cols(ph, col0, ncols);
+        // (two items a round: this runs inside the main loop, where registers are scarce)
+        for (int round = 0; round < M * (ncols >> 3); round += 2 * kGemvThreads) {
+            XStage<2> S;
+            stage_issue(ph, round, S);
+            stage_commit(ph, round, S);
+        }
+    };
     auto fold_group = [&](int ph, int g, const typename F::Raw (&R)[U]) {
-        if (g == 0) {  // first group of a phase: stage its activations
+        if constexpr (LOCAL) {
+            if (g == 0 && ph > 0) {  // phase 0 is staged before the main loop
+                __syncthreads();
+                stage_all(ph);
+                __syncthreads();
+            }
+        } else if (g == 0) {  // first group of a phase: stage its activations
             const int col0 = ph * pchunks * F::CHUNK_COLS;
             const int ncols = min(pchunks * F::CHUNK_COLS, W.g.cols - col0);
             __syncthreads();
@@ -334,32 +435,54 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
         }
     };
 
-    typename F::Raw ra[U], rb[U];
-    // (ph, g) of the group being folded; the next group's loads go out first
-    int ph = 0, g = 0;
-    auto advance = [&](int& p, int& q) {
-        if (++q == gpp) { q = 0; ++p; }
+    // Weights of the next DEPTH - 1 groups are in flight while a group is
+    // folded.  Past the last group the loads repeat the last group (cache
+    // hits): unconditional loads keep the compiler's waits exact.
+    constexpr int DEPTH = TQ_GEMV_DEPTH;
+    static_assert(DEPTH == 2 || DEPTH == 3, "load depth");
+    typename F::Raw rbuf[DEPTH][U];
+    auto load_q = [&](int q, typename F::Raw (&R)[U]) {
+        q = q < ngroups ? q : ngroups - 1;
+        const int p = q / gpp;
+        load_group(p, q - p * gpp, R);
+    };
+    auto fold_q = [&](int q, const typename F::Raw (&R)[U]) {
+        const int p = q / gpp;
+        fold_group(p, q - p * gpp, R);
     };
 #ifdef TQ_GEMV_TRACE
     const unsigned long long tr0 = __builtin_amdgcn_s_memrealtime();
+    unsigned long long tr_a = 0;
 #endif
-    load_group(0, 0, ra);
-    for (int n = 0; n < ngroups; n += 2) {
-        int ph1 = ph, g1 = g;
-        advance(ph1, g1);
-        // past the last group the loads repeat the previous group (cache
-        // hits): unconditional loads keep the waits exact
-        const bool has1 = n + 1 < ngroups;
-        load_group(has1 ? ph1 : ph, has1 ? g1 : g, rb);
-        fold_group(ph, g, ra);
-        if (!has1) break;
-        int ph2 = ph1, g2 = g1;
-        advance(ph2, g2);
-        const bool has2 = n + 2 < ngroups;
-        load_group(has2 ? ph2 : ph1, has2 ? g2 : g1, ra);
-        fold_group(ph1, g1, rb);
-        ph = ph2;
-        g = g2;
+    if constexpr (LOCAL) {
+        // the activations' loads go out ahead of the first weights
+        XStage<kStageItems> S;
+        stage_issue(0, 0, S);
+#pragma unroll
+        for (int d = 0; d < DEPTH - 1; d++) load_q(d, rbuf[d]);
+        stage_commit(0, 0, S);
+        int col0, ncols;
+        phase_cols(0, col0, ncols);
+        for (int round = kStageItems * kGemvThreads; round < M * (ncols >> 3);
+             round += kStageItems * kGemvThreads) {
+            stage_issue(0, round, S);
+            stage_commit(0, round, S);
+        }
+        __syncthreads();
+    } else {
+#pragma unroll
+        for (int d = 0; d < DEPTH - 1; d++) load_q(d, rbuf[d]);
+    }
+    for (int n = 0; n < ngroups; n += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; d++) {
+            if (n + d >= ngroups) break;
+            load_q(n + d + DEPTH - 1, rbuf[(d + DEPTH - 1) % DEPTH]);
+            fold_q(n + d, rbuf[d]);
+#ifdef TQ_GEMV_TRACE
+            if (n + d == 0) tr_a = __builtin_amdgcn_s_memrealtime();
+#endif
+        }
     }
 
 #ifdef TQ_GEMV_TRACE
@@ -425,7 +548,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             t[0] = tr0;
             t[1] = tr1;
             t[2] = __builtin_amdgcn_s_memrealtime();
-            t[3] = ((unsigned long long)(pi | (part << 8) | ((xcc & 15) << 16)) << 32) | hw;
+            t[3] = ((unsigned long long)(pi | (part << 8) | ((xcc & 15) << 16) | ((unsigned)((tr_a - tr0) / 10 < 255ull ? (tr_a - tr0) / 10 : 255ull) << 24)) << 32) | hw;
         }
     }
 #endif
@@ -517,7 +640,11 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
     int order[TITAN_MAX_BATCH];
     for (int i = 0; i < a.n; i++) order[i] = i;
     for (int i = 1; i < a.n; i++)
+#ifdef TQ_GEMV_ORDER_ASC
+        for (int k2 = i; k2 > 0 && a.p[order[k2]].nchunks < a.p[order[k2 - 1]].nchunks; k2--) {
+#else
         for (int k2 = i; k2 > 0 && a.p[order[k2]].nchunks > a.p[order[k2 - 1]].nchunks; k2--) {
+#endif
             int t = order[k2]; order[k2] = order[k2 - 1]; order[k2 - 1] = t;
         }
     GemvArgs b = a;
