@@ -256,11 +256,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int cc = chunk_at(ph, g, u);
-#ifdef TQ_GEMV_NOLOAD
-            F::template load<GS>(W, off, 0, j, R[u]);
-#else
             F::template load<GS>(W, off, cc < nchunks ? cc : 0, j, R[u]);
-#endif
         }
         if constexpr (has_sb_cell<F>()) {
             static_assert(U % GS == 0, "a chunk group holds whole scale cells");
@@ -640,11 +636,7 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
     int order[TITAN_MAX_BATCH];
     for (int i = 0; i < a.n; i++) order[i] = i;
     for (int i = 1; i < a.n; i++)
-#ifdef TQ_GEMV_ORDER_ASC
-        for (int k2 = i; k2 > 0 && a.p[order[k2]].nchunks < a.p[order[k2 - 1]].nchunks; k2--) {
-#else
         for (int k2 = i; k2 > 0 && a.p[order[k2]].nchunks > a.p[order[k2 - 1]].nchunks; k2--) {
-#endif
             int t = order[k2]; order[k2] = order[k2 - 1]; order[k2 - 1] = t;
         }
     GemvArgs b = a;
