@@ -42,7 +42,9 @@ enum {
     TITAN_ERR_INVALID_ARG = -1,   /* null pointer, non-positive size, bad enum */
     TITAN_ERR_UNSUPPORTED = -2,   /* shape / format / layout combination */
     TITAN_ERR_LAUNCH = -3,        /* hipGetLastError() after the launch */
-    TITAN_ERR_WORKSPACE = -4      /* workspace missing or too small */
+    TITAN_ERR_WORKSPACE = -4,     /* workspace missing or too small */
+    TITAN_ERR_IO = -5,            /* checkpoint file missing, unreadable or malformed */
+    TITAN_ERR_NOT_FOUND = -6      /* no such tensor in the checkpoint */
 };
 
 /* ---- element / weight formats --------------------------------------------

@@ -235,3 +235,19 @@ def test_sparse_dequant_matvec_int4(rows, cols, gs, nact, rng):
     assert np.all(got[~mask] == 7.5)
     if nact:
         assert_close_out(got[mask], ref[mask], "f32")
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("fmt,rows,cols,gs", [("int4", 32, 1024, 256), ("int4", 16, 640, 128),
+                                              ("int4", 48, 512, 32), ("int4", 64, 14336, 128),
+                                              ("int2", 16, 1024, 512), ("int2", 32, 768, 128)])
+def test_scale_cells_and_k_split(fmt, rows, cols, gs, M, rng):
+    """Tiled INT4 / INT2 scales in 16-byte cells (groups over several chunks,
+    padded cells, several groups per chunk) and long rows whose chunks are
+    split between the waves of a workgroup."""
+    d = make_weights(fmt, rows, cols, rng, gs=gs)
+    W = upload(d, tq.LAYOUT_TILED)
+    x, x64 = act(M, cols, "f16", rng)
+    y = tq.qgemm(W, x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close_out(to_np(y), x64 @ d["deq"].astype(np.float64).T, "f32")

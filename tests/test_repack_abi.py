@@ -91,3 +91,20 @@ def test_repack_rejects_untileable_shapes():
     with pytest.raises(tq.TitanError):
         tq.repack_host(tq.INT4, 15, 256, np.zeros((15, 32), np.uint32),
                        np.zeros((15, 4), np.uint16), np.zeros((15, 4), np.uint16), 64)
+
+
+@pytest.mark.parametrize("fmt,rows,cols,gs", [("int4", 32, 1024, 256),   # a group over two chunks
+                                              ("int4", 16, 640, 128),    # five groups: padded scale cell
+                                              ("int4", 16, 512, 32),     # four groups per chunk
+                                              ("int2", 16, 1024, 512),   # two chunks per group
+                                              ("int2", 32, 768, 128)])   # three chunks: padded cell
+def test_repack_roundtrip_scale_cells(fmt, rows, cols, gs, rng):
+    """INT4 / INT2 scales sit in 16-byte cells (repeated for groups longer
+    than a chunk, padded to whole cells); the round trip stays exact."""
+    d = make_weights(fmt, rows, cols, rng, gs=gs)
+    f = FMTS[fmt]
+    n = tq.tiled_bytes(f, rows, cols, gs)
+    assert n > 0
+    t = tq.repack_host(f, rows, cols, d["codes"], d["scales"], d["biases"], gs)
+    c2, s2, b2 = tq.unpack_host(f, rows, cols, t, d["codes"], d["scales"], d["biases"], gs)
+    assert np.array_equal(c2, d["codes"]) and np.array_equal(s2, d["scales"]) and np.array_equal(b2, d["biases"])

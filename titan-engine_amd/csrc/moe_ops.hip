@@ -316,6 +316,8 @@ extern "C" const char* titan_status_string(int s) {
         case TITAN_ERR_UNSUPPORTED: return "unsupported shape/format/layout";
         case TITAN_ERR_LAUNCH: return "kernel launch failed";
         case TITAN_ERR_WORKSPACE: return "workspace missing or too small";
+        case TITAN_ERR_IO: return "checkpoint file missing, unreadable or malformed";
+        case TITAN_ERR_NOT_FOUND: return "tensor not found";
         default: return "unknown status";
     }
 }

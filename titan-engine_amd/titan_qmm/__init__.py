@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(HERE, "libtitan_qmm.so")
 
 # status / enums (include/titan_qmm.h)
 OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_WORKSPACE = 0, -1, -2, -3, -4
+ERR_IO, ERR_NOT_FOUND = -5, -6
 FP32, FP16, BF16 = 0, 1, 2
 FP8_E4M3, FP4, INT4, INT2, Q4_K, Q3_K, NVFP4 = 3, 5, 7, 8, 9, 10, 32
 LAYOUT_REF, LAYOUT_TILED = 0, 1
@@ -37,6 +38,23 @@ class QWeightC(ctypes.Structure):
 
 class TitanError(RuntimeError):
     pass
+
+
+# checkpoint reader (include/titan_ckpt.h)
+CK_F32, CK_F16, CK_BF16, CK_F64, CK_I8, CK_U8, CK_I16, CK_I32, CK_I64, CK_BOOL = range(10)
+CK_F8_E4M3, CK_F8_E5M2, CK_GGML, CK_INT4_AFFINE = 10, 11, 100, 200
+
+
+class CkTensorC(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_int), ("ggml_type", ctypes.c_int),
+                ("ndim", ctypes.c_int), ("shape", ctypes.c_int64 * 8), ("nbytes", ctypes.c_uint64),
+                ("group_size", ctypes.c_int)]
+
+
+class CkWeightC(ctypes.Structure):
+    _fields_ = [("format", ctypes.c_int), ("rows", ctypes.c_int), ("cols", ctypes.c_int),
+                ("group_size", ctypes.c_int), ("global_scale", ctypes.c_float),
+                ("tiled_bytes", ctypes.c_size_t)]
 
 
 _LIB = None
@@ -66,6 +84,13 @@ _SIGS = {
     "titan_moe_nvfp4_workspace_bytes": [_I, _I, _I, _I, _I],
     "titan_moe_nvfp4_forward": [_P, _I, _I, _I, _P, _I, _I, _P, _P, _I, _P, _P, _F, _P, _I,
                                 _P, _SZ, _P],
+    "titan_ckpt_open": [ctypes.c_char_p, ctypes.POINTER(_P)],
+    "titan_ckpt_count": [_P],
+    "titan_ckpt_tensor_at": [_P, _I, ctypes.POINTER(CkTensorC)],
+    "titan_ckpt_find": [_P, ctypes.c_char_p],
+    "titan_ckpt_read": [_P, _I, _P, _SZ],
+    "titan_ckpt_weight_info": [_P, ctypes.c_char_p, ctypes.POINTER(CkWeightC)],
+    "titan_ckpt_load_tiled": [_P, ctypes.c_char_p, _P, _SZ, ctypes.POINTER(CkWeightC)],
     "titan_version": [],
     "titan_status_string": [_I],
 }
@@ -82,6 +107,8 @@ def lib():
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = _I
+        L.titan_ckpt_close.argtypes = [_P]
+        L.titan_ckpt_close.restype = None
         L.titan_tiled_bytes.restype = _SZ
         L.titan_moe_nvfp4_workspace_bytes.restype = _SZ
         L.titan_version.restype = ctypes.c_char_p
@@ -337,3 +364,82 @@ def moe_nvfp4_forward(table, E, hidden, inter, x, indices, weights, out, workspa
                                          _ptr(out), dtype_code(out.dtype), _ptr(workspace),
                                          workspace.numel() * workspace.element_size(),
                                          _stream(stream)), "moe_nvfp4_forward")
+
+
+# ---------------------------------------------------------------------------
+# checkpoints: safetensors / GGUF / titan-v1 reads and load-time repack
+# ---------------------------------------------------------------------------
+class Checkpoint:
+    """A checkpoint opened through titan_ckpt_open (a .safetensors or .gguf
+    file, or a directory of safetensors shards or a titan-v1 manifest).
+
+    ``load_tiled(name)`` returns the TILED host buffer of a quantized weight
+    (GGUF Q4_K / Q3_K, titan-v1 int4, or an NVFP4 projection given by its base
+    name) and its description; ``load_weight(name)`` uploads it as a QWeight."""
+
+    def __init__(self, path):
+        h = _P()
+        _check(lib().titan_ckpt_open(os.fsencode(str(path)), ctypes.byref(h)), f"open {path}")
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib().titan_ckpt_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __len__(self):
+        return int(lib().titan_ckpt_count(self._h))
+
+    def tensor(self, index):
+        t = CkTensorC()
+        _check(lib().titan_ckpt_tensor_at(self._h, int(index), ctypes.byref(t)), "tensor_at")
+        return dict(name=t.name.decode(), dtype=t.dtype, ggml_type=t.ggml_type,
+                    shape=tuple(t.shape[d] for d in range(t.ndim)), nbytes=int(t.nbytes),
+                    group_size=t.group_size)
+
+    def tensors(self):
+        return [self.tensor(i) for i in range(len(self))]
+
+    def find(self, name):
+        return int(lib().titan_ckpt_find(self._h, name.encode()))
+
+    def read(self, name_or_index):
+        i = name_or_index if isinstance(name_or_index, int) else self.find(name_or_index)
+        if i < 0:
+            raise TitanError(f"{name_or_index}: status {ERR_NOT_FOUND} (tensor not found)")
+        out = np.empty(self.tensor(i)["nbytes"], np.uint8)
+        _check(lib().titan_ckpt_read(self._h, i, _ptr(out), out.nbytes), "read")
+        return out
+
+    def weight_info(self, name):
+        w = CkWeightC()
+        _check(lib().titan_ckpt_weight_info(self._h, name.encode(), ctypes.byref(w)), f"weight {name}")
+        return dict(fmt=w.format, rows=w.rows, cols=w.cols, group_size=w.group_size,
+                    global_scale=w.global_scale, tiled_bytes=int(w.tiled_bytes))
+
+    def load_tiled(self, name):
+        info = self.weight_info(name)
+        out = np.empty(info["tiled_bytes"], np.uint8)
+        w = CkWeightC()
+        _check(lib().titan_ckpt_load_tiled(self._h, name.encode(), _ptr(out), out.nbytes,
+                                           ctypes.byref(w)), f"load {name}")
+        return out, info
+
+    def load_weight(self, name, device="cuda"):
+        import torch
+        buf, info = self.load_tiled(name)
+        dev = torch.from_numpy(buf).to(device)
+        return QWeight(info["fmt"], LAYOUT_TILED, info["rows"], info["cols"], dev,
+                       group_size=info["group_size"], global_scale=info["global_scale"])
