@@ -216,6 +216,20 @@ int titan_moe_nvfp4_forward(const titan_nvfp4_expert* experts, int num_experts, 
                             hipStream_t stream);
 
 /* ---- library info -------------------------------------------------------- */
+/* Dense GEMV, fp32 activations and output (gemv.cu:33-159):
+ * BF16 A [rows][cols] (gemv_bf16_to_fp32, gemv.cu:103-159), fp32 A (gemv_fp32,
+ * gemv.cu:33-52), and gemv_fp32_batched (gemv.cu:54-72: rows * batch rows of A
+ * against one x, as the reference's single sgemv call computes). */
+int titan_gemv_bf16_to_fp32(const void* A, const float* x, float* y, int rows, int cols,
+                            hipStream_t stream);
+int titan_gemv_fp32(const float* A, const float* x, float* y, int rows, int cols, hipStream_t stream);
+int titan_gemv_fp32_batched(const float* A, const float* x, float* y, int rows, int cols, int batch,
+                            hipStream_t stream);
+/* matvec_dispatch (dense.cpp:13-32), format-exact: W->format selects the
+ * decoder (INT4, INT2, FP4, NVFP4, Q4_K, Q3_K, FP8_E4M3; TITAN_FP32 / TITAN_BF16
+ * for dense row-major weights in W->codes).  fp32 input[cols] -> output[rows]. */
+int titan_matvec_dispatch(const titan_qweight* W, const float* input, float* output, hipStream_t stream);
+
 const char* titan_version(void);
 const char* titan_status_string(int status);
 

@@ -91,6 +91,10 @@ _SIGS = {
     "titan_ckpt_read": [_P, _I, _P, _SZ],
     "titan_ckpt_weight_info": [_P, ctypes.c_char_p, ctypes.POINTER(CkWeightC)],
     "titan_ckpt_load_tiled": [_P, ctypes.c_char_p, _P, _SZ, ctypes.POINTER(CkWeightC)],
+    "titan_gemv_bf16_to_fp32": [_P, _P, _P, _I, _I, _P],
+    "titan_gemv_fp32": [_P, _P, _P, _I, _I, _P],
+    "titan_gemv_fp32_batched": [_P, _P, _P, _I, _I, _I, _P],
+    "titan_matvec_dispatch": [ctypes.POINTER(QWeightC), _P, _P, _P],
     "titan_version": [],
     "titan_status_string": [_I],
 }
@@ -278,6 +282,29 @@ def dequant_matvec_fp4(w, s, x, y, rows, cols, gs, stream=None):
 def dequant_matvec_nvfp4(w, s, g, x, y, rows, cols, stream=None):
     _check(lib().titan_dequant_matvec_nvfp4(_ptr(w), _ptr(s), float(g), _ptr(x), _ptr(y), rows,
                                             cols, _stream(stream)), "dequant_matvec_nvfp4")
+
+
+def gemv_bf16_to_fp32(A, x, y, rows, cols, stream=None):
+    """gemv.cu:103-159: y = bf16(A) @ x, fp32 x / y (A passed as a bf16 or int16 tensor)."""
+    _check(lib().titan_gemv_bf16_to_fp32(_ptr(A), _ptr(x), _ptr(y), rows, cols, _stream(stream)),
+           "gemv_bf16_to_fp32")
+
+
+def gemv_fp32(A, x, y, rows, cols, stream=None):
+    _check(lib().titan_gemv_fp32(_ptr(A), _ptr(x), _ptr(y), rows, cols, _stream(stream)), "gemv_fp32")
+
+
+def gemv_fp32_batched(A, x, y, rows, cols, batch, stream=None):
+    _check(lib().titan_gemv_fp32_batched(_ptr(A), _ptr(x), _ptr(y), rows, cols, batch,
+                                         _stream(stream)), "gemv_fp32_batched")
+
+
+def matvec_dispatch(W, x, y, stream=None):
+    """dense.cpp:13-32, format-exact: W is a QWeight (quantized, or fmt FP32 /
+    BF16 with the dense matrix in ``codes``); fp32 x [cols] -> fp32 y [rows]."""
+    c = W.cstruct()
+    _check(lib().titan_matvec_dispatch(ctypes.byref(c), _ptr(x), _ptr(y), _stream(stream)),
+           "matvec_dispatch")
 
 
 def sparse_dequant_matvec_int4(w, s, b, x, y, active, cols, gs, stream=None):
