@@ -13,7 +13,7 @@
  *   titan_dequant_matvec_fp4    src/compute/dispatch.h:107-109 (fp4.cu:147-159)
  *   titan_dequant_matvec_nvfp4  src/compute/dispatch.h:110-112 (fp4.cu:240-252)
  *   titan_quantize_fp4          src/compute/dispatch.h:113-114 (fp4.cu:254-266)
- *   titan_sparse_dequant_matvec_int4 src/compute/dispatch.h:132-134 (sparse.cu:142-205)
+ *   titan_sparse_dequant_matvec_int4 src/compute/dispatch.h:127-130 (sparse.cu:142-205)
  *   titan_moe_gate              src/compute/dispatch.h:82-83   (moe.cu:197-205)
  *   titan_moe_topk              src/compute/dispatch.h:84-85   (moe.cu:207-214)
  *   titan_swiglu                src/compute/dispatch.h:47-48   (activation.cu:145-151)
@@ -104,7 +104,7 @@ int titan_dequant_matvec_fp4(const void* weights, const void* scales, const floa
 int titan_dequant_matvec_nvfp4(const void* weights, const void* scales, float global_scale,
                                const float* input, float* output, int rows, int cols,
                                hipStream_t stream);
-/* sparse.cu:142-205 (dispatch.h:132-134): output[active_indices[i]] =
+/* sparse.cu:142-205 (dispatch.h:127-130): output[active_indices[i]] =
  * dot(W[row], input) for the listed rows only (REF INT4 layout, fp32 in and
  * out); other outputs are left untouched.  Indices must be valid rows. */
 int titan_sparse_dequant_matvec_int4(const void* weights, const void* scales, const void* biases,

@@ -1,6 +1,6 @@
 // sparse.hip -- activation-sparse INT4 GEMV: only the rows listed in
 // active_indices are computed (sparse.cu:142-205 sparse_dequant_matvec_int4,
-// declared in dispatch.h:132-134).  output[active_indices[i]] = dot(W[row], x)
+// declared in dispatch.h:127-130).  output[active_indices[i]] = dot(W[row], x)
 // with W dequantized as q * s + b (fp16 scale / bias per group); every other
 // output element is left untouched, as in the reference.
 //
@@ -67,7 +67,7 @@ __global__ __launch_bounds__(256) void sparse_int4_kernel(const uint32_t* __rest
 
 }  // namespace tq
 
-// dispatch.h:132-134 (titan::cuda::sparse_dequant_matvec_int4).  As in the
+// dispatch.h:127-130 (titan::cuda::sparse_dequant_matvec_int4).  As in the
 // reference call there is no row count: indices must be valid rows of the
 // weight buffer (negative ones are skipped).
 extern "C" int titan_sparse_dequant_matvec_int4(const void* weights, const void* scales,
