@@ -152,3 +152,33 @@ def test_moe_nvfp4_rejects_bad_args(rng):
                      device="cuda")
     with pytest.raises(tq.TitanError):   # inter not a multiple of 512
         tq.moe_nvfp4_forward(table, E, hidden, 384, x, idx, w, out, ws)
+
+
+def test_moe_nvfp4_every_scale_byte(rng):
+    """Every E4M3 block-scale byte, NaNs (0x7F / 0xFF -> 0, fp4.cu:173-185)
+    and subnormals included, decodes exactly in the grouped GEMM."""
+    E, hidden, inter, T, k = 4, 512, 512, 6, 2
+    ex = []
+    for e in range(E):
+        mats = {}
+        for name, (n, kk) in (("gate", (inter, hidden)), ("up", (inter, hidden)), ("down", (hidden, inter))):
+            w = rng.integers(0, 256, (n, kk // 2), dtype=np.uint8)
+            s = ((np.arange(n * (kk // 16)) * 7 + 31 * e) % 256).astype(np.uint8).reshape(n, kk // 16)
+            g = 2e-4
+            deq = np.asarray(O.dequant_nvfp4(w, s, g, n, kk), np.float64).reshape(n, kk)
+            t = tq.repack_host(tq.NVFP4, n, kk, w, s, None, 0)
+            mats[name] = dict(w=w, s=s, g=g, deq=deq, dev=torch.from_numpy(t).cuda())
+        ex.append(mats)
+    assert set(np.unique(np.concatenate([m["gate"]["s"].ravel() for m in ex]))) == set(range(256))
+    table = tq.nvfp4_expert_table([(m["gate"]["dev"], m["up"]["dev"], m["down"]["dev"],
+                                    m["gate"]["g"], m["up"]["g"], m["down"]["g"]) for m in ex])
+    idx, w = routing(T, E, k, rng)
+    x = torch.from_numpy(rng.normal(0, 1, (T, hidden)).astype(np.float32)).to(torch.float16)
+    ws = torch.empty(tq.moe_nvfp4_workspace_bytes(T, k, E, hidden, inter), dtype=torch.uint8, device="cuda")
+    out = torch.empty(T, hidden, device="cuda")
+    tq.moe_nvfp4_forward(table, E, hidden, inter, x.cuda(), torch.from_numpy(idx).cuda(),
+                         torch.from_numpy(w).cuda(), out, ws)
+    torch.cuda.synchronize()
+    want = ref_fp64(ex, x.double().numpy(), idx, w, None, None, 0.0)
+    assert np.isfinite(out.cpu().numpy()).all()
+    assert_close_out(out.cpu().numpy().astype(np.float64), want, "f32")

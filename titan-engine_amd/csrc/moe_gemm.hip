@@ -47,17 +47,27 @@ struct MoeGemmArgs {
     int64_t ldo;
 };
 
-// e4m3 byte (fp4.cu:173-185 semantics: 0x7F / 0xFF -> 0) as fp16 bits of
-// value * 2^-8: the exponent fields differ by 8 in bias, so it is a shift.
-TQ_DEV uint32_t e4m3_h16_scaled(uint32_t b) {
-    const uint32_t m = b & 0x7Fu;
-    const uint32_t h = ((b & 0x80u) << 8) | (m << 7);
-    return m == 0x7Fu ? 0u : h;
+// A lane's four E4M3 block scales -- bytes jj and 2 + jj of both 32-bit
+// halves of its 8-byte chunk scale word (sel gathers them) -- as fp16 of
+// value * 2^-8, two per register: the hardware conversion with a 2^-8 scale
+// (exact: E4M3 * 2^-8 is an fp16 normal or subnormal), then the E4M3 NaNs
+// 0x7F / 0xFF, which fp4.cu:173-185 reads as 0, cleared: every finite scale
+// * 2^-8 is below 2, so only a NaN half has exponent bit 14 set.
+TQ_DEV uint32_t clear_nan_halves(uint32_t h) {
+    const uint32_t t = (h & 0x40004000u) >> 14;
+    return h & ~__umul24(t, 0xFFFFu);
+}
+TQ_DEV void e4m3x4_scaled(uint2 sv, uint32_t sel, mh2& s01, mh2& s23) {
+    const uint32_t g = __builtin_amdgcn_perm(sv.y, sv.x, sel);
+    const uint32_t a = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(g, 0.00390625f, false));
+    const uint32_t b = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(g, 0.00390625f, true));
+    s01 = __builtin_bit_cast(mh2, clear_nan_halves(a));
+    s23 = __builtin_bit_cast(mh2, clear_nan_halves(b));
 }
 
 // 8 fp4 codes of one word (low nibble first) times one scale -> B operand.
-TQ_DEV mh8 nvfp4_b8(uint32_t w, uint32_t sc16) {
-    const mh2 s = __builtin_bit_cast(mh2, sc16 | (sc16 << 16));
+TQ_DEV mh8 nvfp4_b8(uint32_t w, _Float16 sc) {
+    const mh2 s = {sc, sc};
     const mh2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 256.0f, 0) * s;
     const mh2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 256.0f, 1) * s;
     const mh2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 256.0f, 2) * s;
@@ -70,7 +80,7 @@ TQ_DEV mh8 nvfp4_b8(uint32_t w, uint32_t sc16) {
 // all of them).  GATED: gate and up together with the SwiGLU epilogue;
 // otherwise one matrix, fp32 rows out.
 template <int TM, int SL, int RT, bool GATED, int XDT>
-__global__ __launch_bounds__(kMoeThreads) void moe_gemm_kernel(MoeGemmArgs a) {
+__global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(2))) void moe_gemm_kernel(MoeGemmArgs a) {
     constexpr int NB = TM / 16;         // MFMA token blocks
     constexpr int CPS = SL / 128;       // 64-byte chunks per slab
     constexpr int LDR = SL + 8;         // halves per LDS row (16 B pad)
@@ -98,7 +108,9 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemm_kernel(MoeGemmArgs a) {
         sc_off[q] = (uint32_t)tiled_nvs_off(geo, row0(q) + r, 0);
     }
     const int nslab = a.K / SL;
-    const int sh = 8 * (j >> 1);  // byte of the lane's scale within a half chunk
+    // bytes of the lane's scales in its chunk scale word (see e4m3x4_scaled)
+    const uint32_t jj = (uint32_t)(j >> 1);
+    const uint32_t ssel = jj | ((2 + jj) << 8) | ((4 + jj) << 16) | ((6 + jj) << 24);
 
     for (int t0 = 0; t0 < n_e; t0 += TM) {
         const int nt = min(TM, n_e - t0), nb = (nt + 15) >> 4;
@@ -160,17 +172,11 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemm_kernel(MoeGemmArgs a) {
             __syncthreads();
 #pragma unroll
             for (int c = 0; c < CPS; c++) {
-                uint32_t scw[NM][RT][4];
+                mh2 scw[NM][RT][2];  // word i's scale: half i % 2 of scw[.][.][i / 2]
 #pragma unroll
                 for (int m = 0; m < NM; m++)
 #pragma unroll
-                    for (int q = 0; q < RT; q++) {
-                        const uint2 sv = wc.s[m][q][c];
-                        scw[m][q][0] = e4m3_h16_scaled((sv.x >> sh) & 0xFFu);
-                        scw[m][q][1] = e4m3_h16_scaled((sv.x >> (16 + sh)) & 0xFFu);
-                        scw[m][q][2] = e4m3_h16_scaled((sv.y >> sh) & 0xFFu);
-                        scw[m][q][3] = e4m3_h16_scaled((sv.y >> (16 + sh)) & 0xFFu);
-                    }
+                    for (int q = 0; q < RT; q++) e4m3x4_scaled(wc.s[m][q][c], ssel, scw[m][q][0], scw[m][q][1]);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     mh8 B[NM][RT];
@@ -180,7 +186,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemm_kernel(MoeGemmArgs a) {
                         for (int q = 0; q < RT; q++) {
                             const uint4 cw = wc.c[m][q][c];
                             const uint32_t w = i == 0 ? cw.x : i == 1 ? cw.y : i == 2 ? cw.z : cw.w;
-                            B[m][q] = nvfp4_b8(w, scw[m][q][i]);
+                            B[m][q] = nvfp4_b8(w, scw[m][q][i >> 1][i & 1]);
                         }
 #pragma unroll
                     for (int b = 0; b < NB; b++) {
