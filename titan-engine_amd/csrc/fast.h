@@ -602,7 +602,9 @@ struct FxNvfp4 {
     TQ_DEV static void issue(const Raw&, int, const _Float16* const*, Tmp<NB, GS, SX>&) {}
     template <int NB, int NV, int GS, bool SX>
     TQ_DEV static void finish(const Tmp<NB, GS, SX>&, const Dec&, const float*, f4_t*) {}
+    static constexpr bool STAGE_LOCAL = true;
     TQ_DEV static uint4 stage8(const _Float16* xr, int d0) { return FxNib<LAYOUT, true>::stage8(xr, d0); }
+    TQ_DEV static uint4 stage8_raw(uint4 raw) { return FxNib<LAYOUT, true>::stage8_raw(raw); }
     TQ_DEV static int steps_per_group(const WDesc&) { return 1; }
     template <int GS> static constexpr int sx_cols() { return 32; }
 };
@@ -995,9 +997,11 @@ struct FxFp8 {
     TQ_DEV static void issue(const Raw&, int, const _Float16* const*, Tmp<NB, GS, SX>&) {}
     template <int NB, int NV, int GS, bool SX>
     TQ_DEV static void finish(const Tmp<NB, GS, SX>&, const Dec&, const float*, f4_t*) {}
-    TQ_DEV static uint4 stage8(const _Float16* xr, int d0) {
-        _Float16 h[8], o[8];
-        ldh8(xr + d0, h);
+    static constexpr bool STAGE_LOCAL = true;
+    TQ_DEV static uint4 stage8(const _Float16* xr, int d0) { return stage8_raw(*(const uint4*)(xr + d0)); }
+    TQ_DEV static uint4 stage8_raw(uint4 raw) {
+        const h8_t h = h8_of(raw);
+        _Float16 o[8];
         o[0] = h[0]; o[1] = h[2]; o[2] = h[1]; o[3] = h[3];
         o[4] = h[4]; o[5] = h[6]; o[6] = h[5]; o[7] = h[7];
         return pack8(o);

@@ -175,21 +175,21 @@ TQ_DEV typename F::Dec decode_u(const WDesc& W, const RawArr& R, int u, int cc, 
     else return F::template decode<GS>(W, R[u], cc, j);
 }
 
-// Formats whose stage8 permutes only its own 8 columns (STAGE_LOCAL) stage
-// in one round of 16-byte loads per thread, issued before the first weights.
+// Formats whose stage8 permutes only its own 8 columns (STAGE_LOCAL) turn a
+// loaded item into its staged form in registers (stage8_raw).
 template <class F>
 constexpr bool stage_local() {
     if constexpr (has_stage_local<F>::value) return F::STAGE_LOCAL;
     else return false;
 }
-constexpr int kStageItems = 8;
+constexpr int kStageItems = 8;  // 16-byte activation loads per thread and round
 template <int NI>
 struct XStage { uint4 v[NI]; unsigned live; };
 template <class F>
 TQ_DEV uint4 stage8_raw_of(uint4 v) {
     if constexpr (stage_local<F>()) return F::stage8_raw(v);
     else return v;
-}  // 16-byte activation loads per thread and round
+}
 
 #ifdef TQ_GEMV_TRACE
 // diagnostic build only: per-wave timestamps (100 MHz) and hardware ids
@@ -267,11 +267,16 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             }
         }
     };
-    // One-round staging (STAGE_LOCAL formats, fp16 activations): item e of a
-    // phase is token e / nb8, columns [8 (e % nb8), +8); every load of a round
-    // is issued before any is used, and the column sums come from the same
-    // registers (a shuffle over the lanes of one sum window).
-    constexpr bool LOCAL = stage_local<F>() && MODE != kModeF32;
+    // One-round staging (fp16 activations): item e of a phase is token
+    // e / nb8, columns [8 (e % nb8), +8); every load of a round is issued
+    // before any is used (for phase 0 ahead of the first weights), and the
+    // column sums come from the same registers (a shuffle over the lanes of
+    // one sum window).  STAGE_LOCAL formats permute each item in registers;
+    // the others, for one token, store the raw rows and permute them in place
+    // in LDS (with more tokens their multi-phase stages measured faster with
+    // the per-phase staging below).
+    constexpr bool ONE = MODE != kModeF32 && (stage_local<F>() || M == 1);
+    constexpr bool PERM = !stage_local<F>();
     auto phase_cols = [&](int ph, int& col0, int& ncols) {
         col0 = ph * pchunks * F::CHUNK_COLS;
         ncols = min(pchunks * F::CHUNK_COLS, W.g.cols - col0);
@@ -303,7 +308,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             const int e = round + k * kGemvThreads + tid;
             const int m = e / nb8, d = e - m * nb8;
             const uint4 v = (S.live >> k) & 1u ? S.v[k] : make_uint4(0, 0, 0, 0);
-            if (m < M) *(uint4*)(xh + m * pc + 8 * d) = stage8_raw_of<F>(v);
+            if (m < M) *(uint4*)(xh + m * pc + 8 * d) = PERM ? v : stage8_raw_of<F>(v);
             if constexpr (SX || MODE == kModeDot2) {
                 // SX: sums over one scale window at s16[4 * (col / 32) + token];
                 // VALU fold: sums over 16 columns at s16[token * (pc / 16) + col / 16]
@@ -325,6 +330,30 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             }
         }
     };
+    // raw rows -> the format's staged order, in place: every window a stage8
+    // reads lies inside one round, so a round's reads precede its writes
+    auto stage_permute = [&](int ph) {
+        int col0, ncols;
+        phase_cols(ph, col0, ncols);
+        const int nb8 = ncols >> 3;
+        for (int round = 0; round < M * nb8; round += 2 * kGemvThreads) {
+            uint4 o[2];
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int e = round + k * kGemvThreads + tid;
+                const int m = e / nb8, d = e - m * nb8;
+                o[k] = m < M ? F::stage8(xh + m * pc, 8 * d) : make_uint4(0, 0, 0, 0);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int e = round + k * kGemvThreads + tid;
+                const int m = e / nb8, d = e - m * nb8;
+                if (m < M) *(uint4*)(xh + m * pc + 8 * d) = o[k];
+            }
+            __syncthreads();
+        }
+    };
     auto stage_all = [&](int ph) {  // later phases: one round after another
         int col0, ncols;
         phase_cols(ph, col0, ncols);
@@ -334,9 +363,13 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             stage_issue(ph, round, S);
             stage_commit(ph, round, S);
         }
+        if constexpr (PERM) {
+            __syncthreads();
+            stage_permute(ph);
+        }
     };
     auto fold_group = [&](int ph, int g, const typename F::Raw (&R)[U]) {
-        if constexpr (LOCAL) {
+        if constexpr (ONE) {
             if (g == 0 && ph > 0) {  // phase 0 is staged before the main loop
                 __syncthreads();
                 stage_all(ph);
@@ -450,7 +483,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     const unsigned long long tr0 = __builtin_amdgcn_s_memrealtime();
     unsigned long long tr_a = 0;
 #endif
-    if constexpr (LOCAL) {
+    if constexpr (ONE) {
         // the activations' loads go out ahead of the first weights
         XStage<kStageItems> S;
         stage_issue(0, 0, S);
@@ -463,6 +496,10 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
              round += kStageItems * kGemvThreads) {
             stage_issue(0, round, S);
             stage_commit(0, round, S);
+        }
+        if constexpr (PERM) {
+            __syncthreads();
+            stage_permute(0);
         }
         __syncthreads();
     } else {
