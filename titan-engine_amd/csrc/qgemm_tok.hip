@@ -308,7 +308,9 @@ int run_tok_int4(const titan_qweight* Ws, const void* const* Xs, const int64_t* 
 #ifndef TQ_TOK_RT32
 #define TQ_TOK_RT32 2
 #endif
-    if (M <= TQ_TOK_T16) tq::launch_tok_f<16, 4>(a, maxrows, fw, xdt, ydt, st);
+    // one 16-token tile: two row tiles per wave; several token tiles: four
+    if (M <= 16) tq::launch_tok_f<16, 2>(a, maxrows, fw, xdt, ydt, st);
+    else if (M <= TQ_TOK_T16) tq::launch_tok_f<16, 4>(a, maxrows, fw, xdt, ydt, st);
     else if (M <= 32) tq::launch_tok_f<32, TQ_TOK_RT32>(a, maxrows, fw, xdt, ydt, st);
     else tq::launch_tok_f<64, 2>(a, maxrows, fw, xdt, ydt, st);
     return launch_status();
