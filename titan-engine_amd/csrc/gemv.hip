@@ -9,7 +9,7 @@
 namespace {
 
 #ifndef TQ_TOK_MIN
-#define TQ_TOK_MIN 8
+#define TQ_TOK_MIN 9
 #endif
 // token count from which INT4 tiled weights go to the token-tiled kernel
 constexpr int kTokMinTokens = TQ_TOK_MIN;
