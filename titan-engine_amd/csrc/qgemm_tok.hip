@@ -73,10 +73,15 @@ __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) 
     static_assert(4 * XS * 2 >= 4 * RT * NB * 64 * 16, "reduction fits in the stage");
     __shared__ __attribute__((aligned(16))) _Float16 xs_all[4 * XS];
 
+    // blockIdx.x = (row block, token tile) with the token tiles of a row block
+    // 8 workgroups apart: on the same XCD, so the second reads of a row
+    // block's weights come from its L2
     const TokProb P = a.p[blockIdx.y];
-    const int rb0 = blockIdx.x * (16 * RT);
+    const int ntt = (a.M + TM - 1) / TM;
+    const int grp = blockIdx.x / (8 * ntt), rem = blockIdx.x - grp * 8 * ntt;
+    const int rb0 = (grp * 8 + (rem & 7)) * (16 * RT);
     if (rb0 >= P.rows) return;  // uniform per workgroup
-    const int t0 = blockIdx.z * TM;
+    const int t0 = (rem >> 3) * TM;
     const int nt = min(TM, a.M - t0), nb = (nt + 15) >> 4;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -231,7 +236,8 @@ __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) 
 
 template <int TM, int RT, int FW, int XDT, int ODT>
 void launch_tok(const TokArgs& a, int maxrows, hipStream_t st) {
-    dim3 grid((maxrows + 16 * RT - 1) / (16 * RT), TITAN_MAX_BATCH, (a.M + TM - 1) / TM);
+    const int nrb = ((maxrows + 16 * RT - 1) / (16 * RT) + 7) / 8 * 8;
+    dim3 grid(nrb * ((a.M + TM - 1) / TM), TITAN_MAX_BATCH, 1);
     hipLaunchKernelGGL((qgemm_tok_int4_kernel<TM, RT, FW, XDT, ODT>), grid, dim3(kTokThreads), 0, st, a);
 }
 
