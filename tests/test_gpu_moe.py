@@ -92,6 +92,7 @@ def ref_reference_flow(ex, x32, idx, w, residual, shared, sw, hidden, inter):
     (8, 512, 512, 1, 2, "bf16", "f32", False),     # decode, 16-token passes
     (8, 512, 1024, 5, 4, "f16", "bf16", True),
     (8, 1024, 512, 40, 4, "bf16", "f32", True),    # 32-token passes
+    (8, 512, 512, 60, 4, "bf16", "f32", True),     # 48-token passes, experts over 48 tokens
     (8, 512, 512, 70, 8, "f32", "f16", False),     # 64-token passes, an expert over 64 tokens
     (16, 512, 512, 3, 2, "bf16", "f32", False),    # most experts idle
 ])

@@ -421,6 +421,12 @@ int launch_moe(const MoeGemmArgs& a, int x_dtype, int E, hipStream_t st) {
 #ifndef TQ_MOE_D32
 #define TQ_MOE_D32 32, 128, 2
 #endif
+#ifndef TQ_MOE_G48
+#define TQ_MOE_G48 48, 128, 2
+#endif
+#ifndef TQ_MOE_D48
+#define TQ_MOE_D48 48, 128, 4
+#endif
 #ifndef TQ_MOE_G64
 #define TQ_MOE_G64 64, 128, 2
 #endif
@@ -430,8 +436,11 @@ int launch_moe(const MoeGemmArgs& a, int x_dtype, int E, hipStream_t st) {
 #ifndef TQ_MOE_T32
 #define TQ_MOE_T32 8   // mean tokens per expert above which 32-token passes are used
 #endif
+#ifndef TQ_MOE_T48
+#define TQ_MOE_T48 24  // ... 48-token passes
+#endif
 #ifndef TQ_MOE_T64
-#define TQ_MOE_T64 24  // ... and 64-token passes
+#define TQ_MOE_T64 40  // ... and 64-token passes
 #endif
 
 template <bool GATED>
@@ -439,10 +448,12 @@ int launch_moe_tm(int tm, const MoeGemmArgs& a, int x_dtype, int E, hipStream_t 
     if constexpr (GATED) {
         if (tm == 16) return launch_moe<TQ_MOE_G16, true>(a, x_dtype, E, st);
         if (tm == 32) return launch_moe<TQ_MOE_G32, true>(a, x_dtype, E, st);
+        if (tm == 48) return launch_moe<TQ_MOE_G48, true>(a, x_dtype, E, st);
         return launch_moe<TQ_MOE_G64, true>(a, x_dtype, E, st);
     } else {
         if (tm == 16) return launch_moe<TQ_MOE_D16, false>(a, x_dtype, E, st);
         if (tm == 32) return launch_moe<TQ_MOE_D32, false>(a, x_dtype, E, st);
+        if (tm == 48) return launch_moe<TQ_MOE_D48, false>(a, x_dtype, E, st);
         return launch_moe<TQ_MOE_D64, false>(a, x_dtype, E, st);
     }
 }
@@ -483,7 +494,7 @@ extern "C" int titan_moe_nvfp4_forward(const titan_nvfp4_expert* experts, int nu
 
     // tokens per pass from the mean load per expert
     const int avg = (P + num_experts - 1) / num_experts;
-    const int tm = avg <= TQ_MOE_T32 ? 16 : avg <= TQ_MOE_T64 ? 32 : 64;
+    const int tm = avg <= TQ_MOE_T32 ? 16 : avg <= TQ_MOE_T48 ? 32 : avg <= TQ_MOE_T64 ? 48 : 64;
 
     MoeGemmArgs g{};
     g.experts = experts;
