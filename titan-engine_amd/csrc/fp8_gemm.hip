@@ -32,6 +32,9 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+#ifndef TQ_F8_M128
+#define TQ_F8_M128 2  // 256x128 tiles: waves along M (8 waves)
+#endif
 #ifndef TQ_F8_WGN
 #define TQ_F8_WGN 4  // waves along N for the 256-row tiles (8 waves per workgroup)
 #endif
@@ -109,15 +112,15 @@ TQ_DEV void fp8_epilogue(uint8_t* sm, const v16f (&acc)[TI][TJ], int mw, int nw,
 template <int WN, int ODT>
 constexpr int fp8_epilogue_lds(int nwaves) { return nwaves * 32 * (WN * (ODT == TITAN_FP32 ? 4 : 2) + 16); }
 
-template <int BM, int BN, int WGN, int ODT>
-__global__ __launch_bounds__(128 * WGN) void fp8_gemm_kernel(const uint8_t* __restrict__ A,
+template <int BM, int BN, int WGM, int WGN, int ODT>
+__global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(const uint8_t* __restrict__ A,
                                                           const float* __restrict__ sa,
                                                           const uint8_t* __restrict__ W,
                                                           const float* __restrict__ sw,
                                                           void* __restrict__ out, int M, int N,
                                                           int K) {
-    constexpr int NW = 2 * WGN;  // waves: 2 along M x WGN along N
-    constexpr int WM = BM / 2, WN = BN / WGN, TI = WM / 32, TJ = WN / 32;
+    constexpr int NW = WGM * WGN;  // waves: WGM along M x WGN along N
+    constexpr int WM = BM / WGM, WN = BN / WGN, TI = WM / 32, TJ = WN / 32;
     static_assert(TJ >= 1, "wave tile");
     constexpr int ABYTES = BM * kF8BK, BBYTES = BN * kF8BK, SBYTES = ABYTES + BBYTES;
     constexpr int ABLK = BM / 16, BBLK = BN / 16;  // 16-row KiB blocks per stage
@@ -279,30 +282,30 @@ __global__ __launch_bounds__(128 * WGN) void fp8_gemm_kernel(const uint8_t* __re
     fp8_epilogue<WM, WN, TI, TJ, ODT>(sm, acc, m0 + wm * WM, n0 + wn * WN, wave, lane, sa, sw, out, N);
 }
 
-template <int BM, int BN, int WGN, int ODT>
+template <int BM, int BN, int WGM, int WGN, int ODT>
 int launch_fp8_t(const uint8_t* A, const float* sa, const uint8_t* W, const float* sw, void* out,
                  int M, int N, int K, hipStream_t stream) {
     constexpr int lds = kF8Stages * (BM + BN) * kF8BK;
     static bool attr_set = false;  // per kernel; setting it twice is harmless
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)fp8_gemm_kernel<BM, BN, WGN, ODT>,
+        if (hipFuncSetAttribute((const void*)fp8_gemm_kernel<BM, BN, WGM, WGN, ODT>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
             return TITAN_ERR_LAUNCH;
         attr_set = true;
     }
     const int ntiles = (M / BM) * (N / BN);
-    hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, WGN, ODT>), dim3(ntiles), dim3(128 * WGN), lds, stream, A, sa,
+    hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, WGM, WGN, ODT>), dim3(ntiles), dim3(64 * WGM * WGN), lds, stream, A, sa,
                        W, sw, out, M, N, K);
     return tqh::launch_status();
 }
 
-template <int BM, int BN, int WGN>
+template <int BM, int BN, int WGM, int WGN>
 int launch_fp8(const uint8_t* A, const float* sa, const uint8_t* W, const float* sw, void* out,
                int odt, int M, int N, int K, hipStream_t stream) {
     switch (odt) {
-        case TITAN_FP32: return launch_fp8_t<BM, BN, WGN, TITAN_FP32>(A, sa, W, sw, out, M, N, K, stream);
-        case TITAN_FP16: return launch_fp8_t<BM, BN, WGN, TITAN_FP16>(A, sa, W, sw, out, M, N, K, stream);
-        default: return launch_fp8_t<BM, BN, WGN, TITAN_BF16>(A, sa, W, sw, out, M, N, K, stream);
+        case TITAN_FP32: return launch_fp8_t<BM, BN, WGM, WGN, TITAN_FP32>(A, sa, W, sw, out, M, N, K, stream);
+        case TITAN_FP16: return launch_fp8_t<BM, BN, WGM, WGN, TITAN_FP16>(A, sa, W, sw, out, M, N, K, stream);
+        default: return launch_fp8_t<BM, BN, WGM, WGN, TITAN_BF16>(A, sa, W, sw, out, M, N, K, stream);
     }
 }
 
@@ -318,8 +321,8 @@ extern "C" int titan_fp8_gemm(const uint8_t* A, const float* sa, const uint8_t* 
     if ((int64_t)M * K >= (1ll << 31) || (int64_t)N * K >= (1ll << 31)) return TITAN_ERR_UNSUPPORTED;
     // the largest tile that still gives every CU a tile
     if (M % 256 == 0 && N % 256 == 0 && (int64_t)(M / 256) * (N / 256) >= 256)
-        return tq::launch_fp8<256, 256, TQ_F8_WGN>(A, sa, W, sw, out, out_dtype, M, N, K, stream);
+        return tq::launch_fp8<256, 256, 2, TQ_F8_WGN>(A, sa, W, sw, out, out_dtype, M, N, K, stream);
     if (M % 256 == 0 && (int64_t)(M / 256) * (N / 128) >= 256)
-        return tq::launch_fp8<256, 128, TQ_F8_WGN>(A, sa, W, sw, out, out_dtype, M, N, K, stream);
-    return tq::launch_fp8<128, 128, 2>(A, sa, W, sw, out, out_dtype, M, N, K, stream);
+        return tq::launch_fp8<256, 128, TQ_F8_M128, 8 / TQ_F8_M128>(A, sa, W, sw, out, out_dtype, M, N, K, stream);
+    return tq::launch_fp8<128, 128, 2, 2>(A, sa, W, sw, out, out_dtype, M, N, K, stream);
 }
