@@ -188,12 +188,33 @@ __global__ __launch_bounds__(256) void fp8_quant_rows_vec_kernel(const void* __r
             }
         }
     };
+    // rows of up to 16384 elements stay in registers: every load of the row
+    // is in flight at once and the row is read from memory once
+    constexpr int NR = 8;
+    float keep[NR][8];
+    const bool held = K <= NR * 256 * 8;
     float amax = 0.0f;
-    for (int k = tid * 8; k < K; k += 256 * 8) {
-        float v[8];
-        load8(k, v);
+    if (held) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+        for (int r = 0; r < NR; r++) {
+            const int k = (r * 256 + tid) * 8;
+            if (k < K) load8(k, keep[r]);
+            else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) keep[r][i] = 0.0f;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < NR; r++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(keep[r][i]));
+    } else {
+        for (int k = tid * 8; k < K; k += 256 * 8) {
+            float v[8];
+            load8(k, v);
+#pragma unroll
+            for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+        }
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
@@ -202,14 +223,25 @@ __global__ __launch_bounds__(256) void fp8_quant_rows_vec_kernel(const void* __r
     amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float sc = amax > 0.0f ? amax / 448.0f : 1.0f;
     if (tid == 0) xs[m] = sc;
-    for (int k = tid * 8; k < K; k += 256 * 8) {
-        float v[8];
-        load8(k, v);
+    auto put8 = [&](int k, const float* v) {
         uint32_t q[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) q[i] = f32_to_e4m3_rne_sat(v[i] / sc);
         *(uint2*)(xq + base + k) = make_uint2(q[0] | q[1] << 8 | q[2] << 16 | q[3] << 24,
                                               q[4] | q[5] << 8 | q[6] << 16 | q[7] << 24);
+    };
+    if (held) {
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const int k = (r * 256 + tid) * 8;
+            if (k < K) put8(k, keep[r]);
+        }
+    } else {
+        for (int k = tid * 8; k < K; k += 256 * 8) {
+            float v[8];
+            load8(k, v);
+            put8(k, v);
+        }
     }
 }
 
