@@ -70,8 +70,8 @@ __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) 
     constexpr int NI = TM * kTokSlab / 8 / 64;  // staging items per lane
     constexpr int NF = 4 / FW;                  // folds per chunk
     constexpr int XS = TM * kTokLdr;            // halves of one wave's stage
-    static_assert(4 * XS * 2 >= 4 * RT * NB * 64 * 16, "reduction fits in the stage");
-    __shared__ __attribute__((aligned(16))) _Float16 xs_all[4 * XS];
+    constexpr int RED = 4 * RT * NB * 64 * 16 / 2;  // halves of the K-quarter reduction
+    __shared__ __attribute__((aligned(16))) _Float16 xs_all[4 * XS > RED ? 4 * XS : RED];
 
     // blockIdx.x = (row block, token tile) with the token tiles of a row block
     // 8 workgroups apart: on the same XCD, so the second reads of a row
@@ -311,12 +311,18 @@ int run_tok_int4(const titan_qweight* Ws, const void* const* Xs, const int64_t* 
 #ifndef TQ_TOK_T16
 #define TQ_TOK_T16 64     // largest M served by 16-token tiles (one tile per 16 tokens)
 #endif
+#ifndef TQ_TOK_RTA
+#define TQ_TOK_RTA 2
+#endif
+#ifndef TQ_TOK_RTB
+#define TQ_TOK_RTB 4
+#endif
 #ifndef TQ_TOK_RT32
 #define TQ_TOK_RT32 2
 #endif
     // one 16-token tile: two row tiles per wave; several token tiles: four
-    if (M <= 16) tq::launch_tok_f<16, 2>(a, maxrows, fw, xdt, ydt, st);
-    else if (M <= TQ_TOK_T16) tq::launch_tok_f<16, 4>(a, maxrows, fw, xdt, ydt, st);
+    if (M <= 16) tq::launch_tok_f<16, TQ_TOK_RTA>(a, maxrows, fw, xdt, ydt, st);
+    else if (M <= TQ_TOK_T16) tq::launch_tok_f<16, TQ_TOK_RTB>(a, maxrows, fw, xdt, ydt, st);
     else if (M <= 32) tq::launch_tok_f<32, TQ_TOK_RT32>(a, maxrows, fw, xdt, ydt, st);
     else tq::launch_tok_f<64, 2>(a, maxrows, fw, xdt, ydt, st);
     return launch_status();
