@@ -129,7 +129,18 @@ def bench_int4_layer(M, steps, warmup, gen):
     calls = [tq.PreparedBatch(w, Xs, Ys) for w in Ws]
     ms = time_launches(lambda i: calls[i % R](), steps, warmup)
     total = wbytes + abytes
-    return dict(ms=ms, bytes=total, wbytes=wbytes, gbs=total / ms / 1e6, copies=R,
+    # per-launch distribution: an event pair around each of `steps` launches
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for i, (a, b) in enumerate(ev):
+        a.record()
+        calls[i % R]()
+        b.record()
+    torch.cuda.synchronize()
+    each = sorted(a.elapsed_time(b) for a, b in ev)
+    pct = {f"p{q}_us": round(1e3 * each[min(len(each) - 1, int(q / 100 * len(each)))], 2)
+           for q in (10, 50, 90)}
+    return dict(ms=ms, bytes=total, wbytes=wbytes, gbs=total / ms / 1e6, copies=R, pct=pct,
                 layer=layer, flops=2 * M * sum(m["rows"] * m["cols"] for m in layer))
 
 
@@ -436,7 +447,9 @@ def main():
                      "unit": "GB/s", "frac": round(h["gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile(), "kernel": "qgemv_kernel (INT4 tiled, MFMA fold)",
                      "algorithmic_bytes_per_launch": h["bytes"],
-                     "timing": "torch.cuda.Event pair on the launch stream around all timed launches"},
+                     "timing": "torch.cuda.Event pair on the launch stream around all timed launches",
+                     "per_launch": dict(h["pct"], note="event pair around each launch, "
+                                        "includes the launch gap")},
         "cpu_baseline": cpu,
         "cpu_baseline_all_cores": cpu_mt,
         "secondary": secondary,
