@@ -137,3 +137,30 @@ def test_quantize_fp4_bit_exact(rng):
     w_ref, s_ref = O.quantize_fp4(v.reshape(1, -1), gs)
     assert np.array_equal(out.cpu().numpy().view(np.uint32), w_ref.ravel())
     assert np.array_equal(sc.cpu().numpy().view(np.uint16), s_ref.ravel())
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 14336, 4096), (2048, 4096, 14336), (512, 2048, 1024)])
+def test_fp8_gemm_full_size(M, N, K):
+    """The benchmark shapes (256x256 and 256x128 tiles; the small one takes
+    128x128 tiles): every output against a GPU fp32 product of the same e4m3
+    operands, and 8 sampled rows against the oracle (dequant.cu FP8 semantics,
+    fp32 accumulation).  Tolerance: max |out - ref| <= 1e-3 * max |ref| (bf16)."""
+    g = torch.Generator(device="cuda").manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
+    W = torch.randn(N, K, generator=g, device="cuda") * 0.02
+    sw = (W.abs().amax(1) / 448.0).float()
+    wq = (W / sw[:, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+    xq = torch.empty(M, K, dtype=torch.uint8, device="cuda")
+    sa = torch.empty(M, device="cuda")
+    tq.fp8_quantize_rows(x, xq, sa)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    tq.fp8_gemm(xq, sa, wq, sw, out)
+    torch.cuda.synchronize()
+    table = torch.from_numpy(O.e4m3_ref_table()).cuda()
+    a32 = table[xq.long()] * sa[:, None]
+    w32 = table[wq.long()] * sw[:, None]
+    ref = (a32 @ w32.T).double()
+    assert_close_out(out.float().double().cpu().numpy(), ref.cpu().numpy(), "bf16")
+    rows = np.random.default_rng(0).choice(M, 8, replace=False)
+    o8 = O.gemm_fp8(xq.cpu().numpy()[rows], sa.cpu().numpy()[rows], wq.cpu().numpy(), sw.cpu().numpy())
+    assert_close_out(out.float().double().cpu().numpy()[rows], o8.astype(np.float64), "bf16")

@@ -251,3 +251,28 @@ def test_scale_cells_and_k_split(fmt, rows, cols, gs, M, rng):
     y = tq.qgemm(W, x, out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert_close_out(to_np(y), x64 @ d["deq"].astype(np.float64).T, "f32")
+
+
+@pytest.mark.parametrize("M", [1, 8, 32])
+def test_llama8b_layer_full_size(M):
+    """The headline workload at its real size: the seven INT4 g128 matrices of
+    a Llama-3-8B layer in one batched launch against the oracle's fp32 GEMV
+    (dequant.cu:23-104 semantics) on every output, for a sample of tokens."""
+    import bench
+    gen = torch.Generator(device="cuda").manual_seed(11 + M)
+    layer = bench.make_int4_layer(gen)
+    Ws = [tq.QWeight(m["fmt"], tq.LAYOUT_TILED, m["rows"], m["cols"], m["tiled"], group_size=128)
+          for m in layer]
+    X = {k: torch.randn(M, k, generator=gen, device="cuda").half() for k in (4096, 14336)}
+    Xs = [X[m["cols"]] for m in layer]
+    Ys = [torch.empty(M, m["rows"], device="cuda", dtype=torch.float32) for m in layer]
+    tq.qgemm_batched(Ws, Xs, Ys)
+    torch.cuda.synchronize()
+    toks = sorted({0, M - 1, M // 2})
+    for m, y in zip(layer, Ys):
+        w, s, b = (t.cpu().numpy() for t in m["ref"])
+        s16, b16 = s.view(np.uint16), b.view(np.uint16)
+        for t in toks:
+            x32 = X[m["cols"]][t].float().cpu().numpy()
+            ref = O.matvec_fmt_mt("int4", w.view(np.uint32), s16, b16, 1.0, 128, x32, m["rows"], m["cols"], 8)
+            assert_close_out(to_np(y[t]), ref.astype(np.float64), "f32")

@@ -183,3 +183,49 @@ def test_moe_nvfp4_every_scale_byte(rng):
     want = ref_fp64(ex, x.double().numpy(), idx, w, None, None, 0.0)
     assert np.isfinite(out.cpu().numpy()).all()
     assert_close_out(out.cpu().numpy().astype(np.float64), want, "f32")
+
+
+def test_moe_nvfp4_deepseek_size():
+    """The benchmark layer at its real size (256 experts, top-8, hidden 7168,
+    inter 2048, T = 64 with GPU routing): three sampled tokens against the
+    reference's expert loop restated by the oracle (fp4.cu:187-252 GEMVs with
+    the activations rounded to fp16 as they enter the matrix cores, SwiGLU,
+    the fp16 activation the kernel stores, weighted sum in slot order)."""
+    import bench
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    E, hidden, inter, k, T = 256, 7168, 2048, 8, 64
+    mats, table = bench.make_nvfp4_experts(E, hidden, inter, gen)
+    logits = torch.randn(T, E, generator=gen, device="cuda")
+    x = torch.randn(T, hidden, generator=gen, device="cuda").to(torch.bfloat16)
+    wd = torch.empty(T, k, device="cuda")
+    idd = torch.empty(T, k, dtype=torch.int32, device="cuda")
+    tq.moe_topk_batched(logits, wd, idd, k)
+    ws = torch.empty(tq.moe_nvfp4_workspace_bytes(T, k, E, hidden, inter), dtype=torch.uint8, device="cuda")
+    out = torch.empty(T, hidden, device="cuda")
+    tq.moe_nvfp4_forward(table, E, hidden, inter, x, idd, wd, out, ws)
+    torch.cuda.synchronize()
+    g = 0.02 / 448
+    idx, w = idd.cpu().numpy(), wd.cpu().numpy()
+    x16 = x.float().half().float().cpu().numpy()
+    parts = {}
+
+    def ref_parts(e, j, n, kk):
+        if (e, j) not in parts:
+            t = mats[e][j].cpu().numpy()
+            c, s, _ = tq.unpack_host(tq.NVFP4, n, kk, t, np.zeros((n, kk // 2), np.uint8),
+                                     np.zeros((n, kk // 16), np.uint8))
+            parts[(e, j)] = (c, s)
+        return parts[(e, j)]
+
+    for t in (0, 31, 63):
+        acc = np.zeros(hidden, np.float64)
+        for q in range(k):
+            e = int(idx[t, q])
+            gw, gs_ = ref_parts(e, 0, inter, hidden)
+            uw, us = ref_parts(e, 1, inter, hidden)
+            dw, ds = ref_parts(e, 2, hidden, inter)
+            gate = O.matvec_nvfp4(gw, gs_, g, x16[t], inter, hidden)
+            up = O.matvec_nvfp4(uw, us, g, x16[t], inter, hidden)
+            act = O.swiglu(gate, up).astype(np.float16).astype(np.float32)
+            acc += float(w[t, q]) * O.matvec_nvfp4(dw, ds, g, act, hidden, inter).astype(np.float64)
+        assert_close_out(out[t].cpu().numpy().astype(np.float64), acc, "f32")
