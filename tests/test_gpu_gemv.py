@@ -276,3 +276,32 @@ def test_llama8b_layer_full_size(M):
             x32 = X[m["cols"]][t].float().cpu().numpy()
             ref = O.matvec_fmt_mt("int4", w.view(np.uint32), s16, b16, 1.0, 128, x32, m["rows"], m["cols"], 8)
             assert_close_out(to_np(y[t]), ref.astype(np.float64), "f32")
+
+
+@pytest.mark.parametrize("fmt,n,k", [("q4k", 4096, 4096),
+                                     ("q3k", 8192, 8192), ("q3k", 1024, 8192), ("q3k", 28672, 8192),
+                                     ("q3k", 8192, 28672), ("int2", 8192, 8192), ("int2", 1024, 8192),
+                                     ("int2", 28672, 8192), ("int2", 8192, 28672)])
+@pytest.mark.parametrize("M", [1, 4])
+def test_kquant_int2_full_size(fmt, n, k, M):
+    """The Q4_K 4096^2 and Llama-3-70B Q3_K / INT2 g64 benchmark shapes (tiled
+    layout, fp16 tokens) against the oracle's fp32 GEMV of the same REF bytes
+    (ggml block formats; dequant.cu:110-172 for INT2) for every output row."""
+    import bench
+    gen = torch.Generator(device="cuda").manual_seed(n + k + M)
+    if fmt == "int2":
+        (m,) = bench.make_int4_layer(gen, gs=64, bits=2, shapes=[("w", n, k)])
+        W = tq.QWeight(tq.INT2, tq.LAYOUT_TILED, n, k, m["tiled"], group_size=64)
+        w, s, b = (t.cpu().numpy() for t in m["ref"])
+        codes, s16, b16, gs = w.view(np.uint32), s.view(np.uint16), b.view(np.uint16), 64
+    else:
+        f = tq.Q4_K if fmt == "q4k" else tq.Q3_K
+        blk = bench.random_kquant(f, n, k, gen)
+        W = tq.QWeight(f, tq.LAYOUT_TILED, n, k, torch.from_numpy(tq.repack_host(f, n, k, blk)).cuda())
+        codes, s16, b16, gs = blk, None, None, 0
+    x = torch.randn(M, k, generator=gen, device="cuda").half()
+    y = tq.qgemm(W, x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    for t in sorted({0, M - 1}):
+        ref = O.matvec_fmt_mt(fmt, codes, s16, b16, 1.0, gs, x[t].float().cpu().numpy(), n, k, 8)
+        assert_close_out(to_np(y[t]), ref.astype(np.float64), "f32")
