@@ -649,14 +649,23 @@ struct FxQ4K {
     template <int GS>
     TQ_DEV static Dec decode(const WDesc&, const Raw& r, int c, int) {
         const float d = f16_to_f32(r.hdr.x & 0xFFFF), dmin = f16_to_f32(r.hdr.x >> 16);
+        // The four 6-bit scales and mins of this half block, one per byte,
+        // without a branch on the half (ggml packing, scales bytes s[0..11]
+        // in hdr.y/z/w): sub-blocks 0..3 are s[k] & 63 and s[4+k] & 63;
+        // sub-blocks 4..7 take the low / high nibble of s[8+k] and bits 6..7
+        // of s[k] / s[4+k] as their bits 4..5.  Both are (A & 0x0F) |
+        // ((B >> 2) & 0x30) per byte for the right A, B.
+        const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
+        const bool hi = c & 1;
+        const uint32_t a_sc = hi ? s2 : s0, b_sc = hi ? s0 : s0 << 2;
+        const uint32_t a_m = hi ? s2 >> 4 : s1, b_m = hi ? s1 : s1 << 2;
+        const uint32_t SC = (a_sc & 0x0F0F0F0Fu) | ((b_sc >> 2) & 0x30303030u);
+        const uint32_t MN = (a_m & 0x0F0F0F0Fu) | ((b_m >> 2) & 0x30303030u);
         Dec o;
-        const int sb0 = 4 * (c & 1);  // first sub-block of this half block
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            uint32_t sc, m;
-            q4k_scale_min(r.hdr.y, r.hdr.z, r.hdr.w, sb0 + k, sc, m);
-            o.ds[k] = d * (float)sc;
-            o.dm[k] = dmin * (float)m;
+            o.ds[k] = d * (float)((SC >> (8 * k)) & 0xFFu);
+            o.dm[k] = dmin * (float)((MN >> (8 * k)) & 0xFFu);
         }
         return o;
     }
