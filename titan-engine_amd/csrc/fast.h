@@ -792,9 +792,13 @@ struct FxQ3K {
     // sub-block, folded at once with its scale (PIPE = false: issue and
     // finish of a chunk run back to back)
     static constexpr bool HAS_MFMA = true, PIPE = false;
+    // one or two tokens: codes folded in place and the -4 offset applied
+    // from 16-column activation sums (SX); more tokens: codes moved to bit 0
+    // and offset in fp16
+    static constexpr int SX_MAX_M = 2;
     struct Off { uint32_t c, h, s, d; };
     struct Raw { uint32_t w[4]; uint32_t hm0, hm1, s0, s1, s2, dh; };
-    struct Dec { float dsc[4][4]; };  // [i][jj]
+    struct Dec { float dsc[4][4], m4[4][4]; };  // [i][jj]: d (sc - 32), -4 d (sc - 32)
     TQ_DEV static Off base(const WDesc& w, int row, int j) {
         const Geo& g = w.g;
         return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_q3k_hmask_off(g, row, 0, j),
@@ -825,7 +829,7 @@ struct FxQ3K {
             ((r.s0 >> 4) & 0x0F0F0F0Fu) | (((r.s2 >> 4) & 0x03030303u) << 4),  // 8..11
             ((r.s1 >> 4) & 0x0F0F0F0Fu) | (((r.s2 >> 6) & 0x03030303u) << 4)}; // 12..15
         Dec o;
-        const float d = f16_to_f32(r.dh), d32 = -32.0f * d;
+        const float d = f16_to_f32(r.dh), d32 = -32.0f * d, dm4 = -4.0f * d, d128 = 128.0f * d;
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -833,6 +837,7 @@ struct FxQ3K {
                 const int k = 8 * (i >> 1) + 2 * jj + (i & 1);
                 const float sc = (float)((L[k >> 2] >> (8 * (k & 3))) & 0xFFu);
                 o.dsc[i][jj] = __builtin_fmaf(sc, d, d32);
+                o.m4[i][jj] = __builtin_fmaf(sc, dm4, d128);  // exact: -4 is a power of two
             }
         return o;
     }
@@ -896,8 +901,34 @@ struct FxQ3K {
         return j == 0 ? t + bias(d, s16) : t;
     }
     template <int NB, int GS, bool SX> struct Tmp { f4_t C[16][NB]; };
+    // SX: the codes u of level jj in place as fp16 subnormals, u * 2^(2jj-24):
+    // bits 2jj, 2jj+1 of the byte from the 2-bit word, bit 2jj+2 from the
+    // hmask; the halves hold bytes (0, 2) and (1, 3) of the word
+    TQ_DEV static h4_t codes_in_place(const Raw& r, int i, int jj) {
+        const uint32_t w = r.w[i], w8 = w >> 8;
+        const uint32_t hm = (i & 1) ? r.hm1 : r.hm0, hm8 = hm >> 8;
+        const int sh = 4 * (i >> 1) + jj - (2 * jj + 2);  // hmask bit -> bit 2jj+2
+        const uint32_t hb = sh >= 0 ? hm >> sh : hm << -sh, hb8 = sh >= 0 ? hm8 >> sh : hm8 << -sh;
+        const uint32_t mq = 0x00030003u << (2 * jj), mh = 0x00040004u << (2 * jj);
+        return h4_of((w & mq) | (hb & mh), (w8 & mq) | (hb8 & mh));
+    }
     template <int NB, int GS, bool SX>
     TQ_DEV static void issue(const Raw& r, int j, const _Float16* const* xt, Tmp<NB, GS, SX>& T) {
+        if constexpr (SX) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const h4_t b = codes_in_place(r, i, jj);
+#pragma unroll
+                    for (int n = 0; n < NB; n++) {
+                        const _Float16* p = xt[n] + 16 * (8 * (i >> 1) + 4 * (i & 1) + j) + 4 * jj;
+                        const uint2 xv = *(const uint2*)p;
+                        T.C[4 * i + jj][n] = mfma16(h4_of(xv.x, xv.y), b, f4_zero());
+                    }
+                }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -919,7 +950,26 @@ struct FxQ3K {
             }
     }
     template <int NB, int NV, int GS, bool SX>
-    TQ_DEV static void finish(const Tmp<NB, GS, SX>& T, const Dec& d, const float*, f4_t* acc) {
+    TQ_DEV static void finish(const Tmp<NB, GS, SX>& T, const Dec& d, const float* sx, f4_t* acc) {
+        if constexpr (SX) {
+            // sub-block k = 8(i>>1) + 2jj + (i&1): d sc * (C 2^(24-2jj) - 4 sum(x))
+            // = (-4 d sc) * (sum(x) - C 2^(22-2jj)); sums at sx[2k + token]
+            static_assert(NB == 1 && NV <= 2, "SX folds at most two tokens");
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const int k = 8 * (i >> 1) + 2 * jj + (i & 1);
+                    const float2 s2 = *(const float2*)(sx + 2 * k);
+                    const float m4 = d.m4[i][jj], kc = -(float)(1u << (22 - 2 * jj));
+#pragma unroll
+                    for (int v = 0; v < NV; v++) {
+                        const float t = __builtin_fmaf(T.C[4 * i + jj][0][v], kc, v == 0 ? s2.x : s2.y);
+                        acc[0][v] = __builtin_fmaf(m4, t, acc[0][v]);
+                    }
+                }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -943,7 +993,7 @@ struct FxQ3K {
         return pack8(o);
     }
     TQ_DEV static int steps_per_group(const WDesc&) { return 1; }
-    template <int GS> static constexpr int sx_cols() { return 32; }
+    template <int GS> static constexpr int sx_cols() { return 16; }
 };
 
 // ============================================================================

@@ -30,6 +30,28 @@ struct requires_sb_cell : std::false_type {};
 template <class F>
 struct requires_sb_cell<F, std::void_t<decltype(F::SB_CELL)>> : std::true_type {};
 
+template <class F, class = void>
+struct has_sx_max_m : std::false_type {};
+template <class F>
+struct has_sx_max_m<F, std::void_t<decltype(F::SX_MAX_M)>> : std::true_type {};
+
+// Most tokens for which the MFMA fold takes activation sums from LDS (SX)
+// instead of an extra MFMA against ones.  Sums over 32 or more columns keep
+// four tokens per 32 columns; 16-column sums (SX_MAX_M = 2) keep two tokens
+// per 16 columns, in the same space.
+template <class F>
+constexpr int sx_max_m() {
+    if constexpr (has_sx_max_m<F>::value) return F::SX_MAX_M;
+    else return 4;
+}
+// LDS index of the sum of window `b` (SW columns each) for token m
+template <int SW>
+TQ_DEV int sx_index(int b, int m) {
+    static_assert(SW == 16 || SW % 32 == 0, "sum window");
+    if constexpr (SW == 16) return 2 * b + m;
+    else return 4 * (b * (SW / 32)) + m;
+}
+
 #ifndef TQ_GEMV_U
 #define TQ_GEMV_U 4
 #endif
@@ -105,8 +127,9 @@ TQ_DEV void stage_f32(float* xf, float* s16, int pc, const void* x, int xdt, int
 template <int M, int SW>
 TQ_DEV void stage_sums(float* sx, const void* x, int64_t ldx, int m0, int mcount, int col0,
                        int ncols, int tid) {
-    for (int e = tid; e < 4 * (ncols / SW); e += kGemvThreads) {
-        const int b = e >> 2, m = e & 3;
+    constexpr int TPW = SW == 16 ? 2 : 4;  // token slots per window
+    for (int e = tid; e < TPW * (ncols / SW); e += kGemvThreads) {
+        const int b = e / TPW, m = e % TPW;
         float s = 0.0f;
         if (m < mcount && m < M) {
             const _Float16* src = (const _Float16*)x + (int64_t)(m0 + m) * ldx + col0 + SW * b;
@@ -122,7 +145,7 @@ TQ_DEV void stage_sums(float* sx, const void* x, int64_t ldx, int m0, int mcount
             }
             s = a0 + a1;
         }
-        sx[4 * (b * (SW / 32)) + m] = s;
+        sx[sx_index<SW>(b, m)] = s;
     }
 }
 
@@ -224,7 +247,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
 
     constexpr int NB = (M + 15) / 16;  // MFMA token blocks
     constexpr int NV = M < 4 ? M : 4;  // accumulator entries holding tokens
-    constexpr bool SX = MODE == kModeMfma && M <= 4;  // activation sums from LDS
+    constexpr bool SX = MODE == kModeMfma && M <= sx_max_m<F>();  // activation sums from LDS
     f4_t macc[NB];
     float acc[M];
 #pragma unroll
@@ -310,7 +333,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             const uint4 v = (S.live >> k) & 1u ? S.v[k] : make_uint4(0, 0, 0, 0);
             if (m < M) *(uint4*)(xh + m * pc + 8 * d) = PERM ? v : stage8_raw_of<F>(v);
             if constexpr (SX || MODE == kModeDot2) {
-                // SX: sums over one scale window at s16[4 * (col / 32) + token];
+                // SX: sums over one scale window at s16[sx_index(col / window, token)];
                 // VALU fold: sums over 16 columns at s16[token * (pc / 16) + col / 16]
                 constexpr int SW = SX ? F::template sx_cols<GS>() : 16, WL = SW / 8;
                 const h8_t h = h8_of(v);
@@ -324,7 +347,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
 #pragma unroll
                 for (int o = 1; o < WL; o <<= 1) sum += __shfl_xor(sum, o, kWave);
                 if (m < M && d % WL == 0) {
-                    if constexpr (SX) s16[4 * ((8 * d / SW) * (SW / 32)) + m] = sum;
+                    if constexpr (SX) s16[sx_index<SW>(8 * d / SW, m)] = sum;
                     else s16[m * (pc >> 4) + d / 2] = sum;
                 }
             }
