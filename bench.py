@@ -8,7 +8,7 @@ the gfx950 tiled layout.  One step = one pass over the seven matrices (one
 batched launch).  `value` = algorithmic bytes per step / time per step.
 
 Secondary lines (same JSON object, key "secondary"): M = 8 / 32 tokens, the
-Q4_K 4096^2 GEMV, Q3_K / INT2 Llama-3-70B decode shapes
+same layer in Q4_K and Q3_K, the Q4_K 4096^2 GEMV, Q3_K / INT2 Llama-3-70B decode shapes
 (configs[4]) and the FP8 prefill GEMMs.
 
 The weight set is replicated so that each step reads a copy that is not in
@@ -147,7 +147,10 @@ def bench_int4_layer(M, steps, warmup, gen):
 def bench_single(W_list, x, y, steps, warmup, algo_bytes):
     import titan_qmm as tq
     R = len(W_list)
-    ms = time_launches(lambda i: tq.qgemm(W_list[i % R], x, out=y), steps, warmup)
+    # arguments bound once per copy: the Python cost of building them per
+    # call would exceed the kernel time of the small shapes
+    calls = [tq.PreparedBatch([w], [x], [y]) for w in W_list]
+    ms = time_launches(lambda i: calls[i % R](), steps, warmup)
     return ms, algo_bytes / ms / 1e6
 
 
@@ -165,6 +168,29 @@ def bench_kquant(fmt, n, k, M, gen, steps, warmup):
     ms, gbs = bench_single(Wl, x, y, steps, warmup, algo)
     del Wl, dev
     return dict(ms=ms, gbs=gbs, bytes=algo)
+
+
+def bench_kquant_layer(fmt, M, gen, steps, warmup):
+    """One Llama-3-8B layer (LLAMA8B shapes) of synthetic Q4_K / Q3_K codes in
+    one batched launch, as the INT4 headline."""
+    import torch
+    import titan_qmm as tq
+    layer = []
+    for name, n, k in LLAMA8B:
+        t = torch.from_numpy(tq.repack_host(fmt, n, k, random_kquant(fmt, n, k, gen))).cuda()
+        layer.append((n, k, t))
+    wbytes = sum(t.numel() for _, _, t in layer)
+    R = copies_for(wbytes)
+    Ws = [[tq.QWeight(fmt, tq.LAYOUT_TILED, n, k, t if c == 0 else t.clone()) for n, k, t in layer]
+          for c in range(R)]
+    X = {k: torch.randn(M, k, generator=gen, device="cuda").half() for k in (4096, 14336)}
+    Xs = [X[k] for _, k, _ in layer]
+    Ys = [torch.empty(M, n, device="cuda", dtype=torch.float16) for n, _, _ in layer]
+    total = wbytes + sum(M * k * 2 + M * n * 2 for n, k, _ in layer)
+    calls = [tq.PreparedBatch(w, Xs, Ys) for w in Ws]
+    ms = time_launches(lambda i: calls[i % R](), steps, warmup)
+    del Ws, calls, layer
+    return dict(ms=ms, gbs=total / ms / 1e6, bytes=total)
 
 
 def bench_int2(n, k, M, gen, steps, warmup):
@@ -382,6 +408,13 @@ def main():
                                   GBps=round(r["gbs"], 1), frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4),
                                   TFLOPS=round(r["flops"] / r["ms"] / 1e9, 2)))
             del r
+        for fmt, nm in ((tq.Q4_K, "Q4_K"), (tq.Q3_K, "Q3_K")):
+            log(f"{nm} Llama-3-8B layer M=1")
+            r = bench_kquant_layer(fmt, 1, gen, K, W)
+            secondary.append(dict(config=f"{nm} Llama-3-8B layer (q,k,v,o,gate,up,down; synthetic codes)",
+                                  M=1, ms=round(r["ms"], 5), GBps=round(r["gbs"], 1),
+                                  frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4)))
+            torch.cuda.empty_cache()
         log("Q4_K 4096x4096")
         r = bench_kquant(tq.Q4_K, 4096, 4096, 1, gen, K, W)
         secondary.append(dict(config="Q4_K 4096x4096 GEMV (synthetic codes)", M=1,
