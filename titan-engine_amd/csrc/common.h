@@ -11,6 +11,20 @@
 
 namespace tq {
 
+// 16-byte load of data that a kernel streams once (quantized weight codes):
+// nontemporal, measured faster than cached loads for the GEMV, the
+// token-tiled GEMM and the MoE expert GEMM (TQ_STREAM_CACHED restores plain
+// loads, for comparison)
+#ifndef TQ_STREAM_CACHED
+typedef uint32_t tq_u32x4 __attribute__((ext_vector_type(4)));
+TQ_DEV uint4 ld_stream_u128(const void* p) {
+    const tq_u32x4 v = __builtin_nontemporal_load((const tq_u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+#else
+TQ_DEV uint4 ld_stream_u128(const void* p) { return *(const uint4*)p; }
+#endif
+
 constexpr int kWave = 64;
 
 // ---- scalar conversions (bit-exact, no library math) -----------------------

@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(const uint8_t* __restri
             const int ee = e < words ? e : 0;  // past the end: a cached word, not folded
 #pragma unroll
             for (int q = 0; q < R; q++)
-                v[q] = *(const uint4*)(rp[q] + (size_t)(c0 + ee * D::PER) * (BF16 ? 2 : 4));
+                v[q] = ld_stream_u128(rp[q] + (size_t)(c0 + ee * D::PER) * (BF16 ? 2 : 4));
         };
         auto fold = [&](int e, const uint4* v) {  // branch-free: words past the end count zero
             const bool live = e < words;

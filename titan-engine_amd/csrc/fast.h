@@ -30,25 +30,6 @@
 
 namespace tq {
 
-// 16-byte weight-code load of the fast GEMV: each byte is read once, so the
-// load is nontemporal (measured faster than cached loads for the streamed
-// weights)
-#ifndef TQ_WEIGHT_CACHED
-typedef uint32_t tq_u32x4 __attribute__((ext_vector_type(4)));
-TQ_DEV uint4 ldw_u128(const uint8_t* p) {
-    const tq_u32x4 v = __builtin_nontemporal_load((const tq_u32x4*)p);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-#else
-TQ_DEV uint4 ldw_u128(const uint8_t* p) { return ld_u128(p); }
-#endif
-// 16-byte scale-cell / block-header load
-#ifdef TQ_SCALE_NT
-TQ_DEV uint4 lds_u128(const uint8_t* p) { return ldw_u128(p); }
-#else
-TQ_DEV uint4 lds_u128(const uint8_t* p) { return ld_u128(p); }
-#endif
-
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
@@ -157,7 +138,7 @@ struct FxNib {
 #pragma unroll
             for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
         } else {
-            uint4 q = ldw_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_stream_u128(w.codes + (o.c + (uint32_t)c * 1024u));
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
         if constexpr (SB_CELL) return;  // load_cell
@@ -196,7 +177,7 @@ struct FxNib {
     // multiples of 4).
     template <int GS>
     TQ_DEV static void load_cell(const WDesc& w, const Off& o, int c, Raw& r) {
-        r.q = lds_u128(w.codes + (o.s + (uint32_t)(c / GS) * 256u));
+        r.q = ld_u128(w.codes + (o.s + (uint32_t)(c / GS) * 256u));
     }
     template <int GS>
     TQ_DEV static Dec decode_cell(const uint4& q, int u) {
@@ -364,7 +345,7 @@ struct FxInt2 {
 #pragma unroll
             for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
         } else {
-            uint4 q = ldw_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_stream_u128(w.codes + (o.c + (uint32_t)c * 1024u));
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
         if constexpr (SB_CELL) return;  // load_cell
@@ -401,7 +382,7 @@ struct FxInt2 {
     // multiples of 4).
     template <int GS>
     TQ_DEV static void load_cell(const WDesc& w, const Off& o, int c, Raw& r) {
-        r.q = lds_u128(w.codes + (o.s + (uint32_t)(c / GS) * 256u));
+        r.q = ld_u128(w.codes + (o.s + (uint32_t)(c / GS) * 256u));
     }
     template <int GS>
     TQ_DEV static Dec decode_cell(const uint4& q, int u) {
@@ -568,7 +549,7 @@ struct FxNvfp4 {
             r.s0 = ld_u32(sp);
             r.s1 = ld_u32(sp + 4);
         } else {
-            uint4 q = ldw_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_stream_u128(w.codes + (o.c + (uint32_t)c * 1024u));
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
             const uint8_t* sp = w.codes + (o.s + (uint32_t)c * 128u);
             r.s0 = ld_u32(sp);
@@ -660,8 +641,8 @@ struct FxQ4K {
 #pragma unroll
             for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (q + 16u * i));
         } else {
-            r.hdr = lds_u128(w.codes + (o.h + blk * 256u));
-            uint4 q = ldw_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            r.hdr = ld_u128(w.codes + (o.h + blk * 256u));
+            uint4 q = ld_stream_u128(w.codes + (o.c + (uint32_t)c * 1024u));
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
     }
@@ -826,7 +807,7 @@ struct FxQ3K {
     template <int GS>
     TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
         const uint32_t b = (uint32_t)c;
-        uint4 q = ldw_u128(w.codes + (o.c + b * 1024u));
+        uint4 q = ld_stream_u128(w.codes + (o.c + b * 1024u));
         r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         const uint8_t* hp = w.codes + (o.h + b * 512u);
         r.hm0 = ld_u32(hp);
@@ -1038,7 +1019,7 @@ struct FxFp8 {
 #pragma unroll
             for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
         } else {
-            uint4 q = ldw_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_stream_u128(w.codes + (o.c + (uint32_t)c * 1024u));
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
     }

@@ -25,19 +25,6 @@
 #include "layout.h"
 #include "xitem.h"
 
-namespace {
-// expert weight codes: streamed, each byte read by one workgroup per token
-// tile, so the loads are nontemporal
-#ifndef TQ_MOE_W_CACHED
-typedef uint32_t moe_u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 ld_codes(const uint8_t* p) {
-    const moe_u32x4 v = __builtin_nontemporal_load((const moe_u32x4*)p);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-#else
-__device__ __forceinline__ uint4 ld_codes(const uint8_t* p) { return *(const uint4*)p; }
-#endif
-}  // namespace
 
 namespace tq {
 
@@ -155,7 +142,7 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
                     for (int c = 0; c < CPS; c++) {
                         const uint32_t ch = (uint32_t)(s * CPS + c);
-                        w.c[m][q][c] = ld_codes(W[m] + code_off[q] + ch * 1024u);
+                        w.c[m][q][c] = ld_stream_u128(W[m] + code_off[q] + ch * 1024u);
                         w.s[m][q][c] = *(const uint2*)(W[m] + sc_off[q] + ch * 128u);
                     }
         };

@@ -64,7 +64,9 @@ TQ_DEV th8 tok_b8(uint32_t w) {
 // own activation slabs (no barrier in the main loop), with a deterministic
 // reduction of the 4 partial sums through LDS at the end.  FW code words (32
 // columns each) per scale fold.
-template <int TM, int RT, int FW, int XDT, int ODT>
+// STREAM: one token tile reads each weight once (nontemporal loads); with
+// more tiles the later tiles re-read the codes from the caches.
+template <int TM, int RT, int FW, int XDT, int ODT, bool STREAM>
 __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) {
     constexpr int NB = TM / 16;
     constexpr int NI = TM * kTokSlab / 8 / 64;  // staging items per lane
@@ -122,7 +124,8 @@ __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) 
     auto load_w = [&](int s, WSet& w) {
 #pragma unroll
         for (int q = 0; q < RT; q++) {
-            w.c[q] = *(const uint4*)(P.w + code_off[q] + (uint32_t)s * 1024u);
+            const uint8_t* cp = P.w + code_off[q] + (uint32_t)s * 1024u;
+            w.c[q] = STREAM ? ld_stream_u128(cp) : *(const uint4*)cp;
 #pragma unroll
             for (int f = 0; f < NF; f++) {
                 // scale slot: one per chunk for groups of a chunk or more, else one per group
@@ -238,7 +241,10 @@ template <int TM, int RT, int FW, int XDT, int ODT>
 void launch_tok(const TokArgs& a, int maxrows, hipStream_t st) {
     const int nrb = ((maxrows + 16 * RT - 1) / (16 * RT) + 7) / 8 * 8;
     dim3 grid(nrb * ((a.M + TM - 1) / TM), TITAN_MAX_BATCH, 1);
-    hipLaunchKernelGGL((qgemm_tok_int4_kernel<TM, RT, FW, XDT, ODT>), grid, dim3(kTokThreads), 0, st, a);
+    if (a.M <= TM)
+        hipLaunchKernelGGL((qgemm_tok_int4_kernel<TM, RT, FW, XDT, ODT, true>), grid, dim3(kTokThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL((qgemm_tok_int4_kernel<TM, RT, FW, XDT, ODT, false>), grid, dim3(kTokThreads), 0, st, a);
 }
 
 template <int TM, int RT, int FW, int XDT>
