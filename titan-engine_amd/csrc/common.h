@@ -24,6 +24,11 @@ TQ_DEV uint4 ld_stream_u128(const void* p) {
 #else
 TQ_DEV uint4 ld_stream_u128(const void* p) { return *(const uint4*)p; }
 #endif
+template <bool NT>
+TQ_DEV uint4 ld_codes_u128(const void* p) {
+    if constexpr (NT) return ld_stream_u128(p);
+    else return *(const uint4*)p;
+}
 
 constexpr int kWave = 64;
 

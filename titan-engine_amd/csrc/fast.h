@@ -132,13 +132,13 @@ struct FxNib {
         else
             return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_sb_off(g, row, 0), 0u};
     }
-    template <int GS>
+    template <int GS, bool NT = true>
     TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
         if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
 #pragma unroll
             for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
         } else {
-            uint4 q = ld_stream_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_codes_u128<NT>(w.codes + (o.c + (uint32_t)c * 1024u));
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
         if constexpr (SB_CELL) return;  // load_cell
@@ -326,7 +326,7 @@ template <int L> using FxFp4 = FxNib<L, true>;
 template <int LAYOUT>
 struct FxInt2 {
     static constexpr int FMT = TITAN_INT2, CHUNK_COLS = 256;
-    static constexpr bool HAS_MFMA = true, PIPE = true;
+    static constexpr bool HAS_MFMA = true, PIPE = true, LAST_CACHED = false;
     static constexpr bool SB_CELL = LAYOUT == TITAN_LAYOUT_TILED;
     struct Off { uint32_t c, s, b; };
     struct Raw { uint32_t w[4], s[4], b[4]; uint4 q; };
@@ -339,13 +339,13 @@ struct FxInt2 {
         else
             return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_sb_off(g, row, 0), 0u};
     }
-    template <int GS>
+    template <int GS, bool NT = true>
     TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
         if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
 #pragma unroll
             for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
         } else {
-            uint4 q = ld_stream_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_codes_u128<NT>(w.codes + (o.c + (uint32_t)c * 1024u));
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
         if constexpr (SB_CELL) return;  // load_cell
@@ -540,7 +540,7 @@ struct FxNvfp4 {
         else
             return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_nvs_off(g, row, 0)};
     }
-    template <int GS>
+    template <int GS, bool NT = true>
     TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
         if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
 #pragma unroll
@@ -549,7 +549,7 @@ struct FxNvfp4 {
             r.s0 = ld_u32(sp);
             r.s1 = ld_u32(sp + 4);
         } else {
-            uint4 q = ld_stream_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_codes_u128<NT>(w.codes + (o.c + (uint32_t)c * 1024u));
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
             const uint8_t* sp = w.codes + (o.s + (uint32_t)c * 128u);
             r.s0 = ld_u32(sp);
@@ -621,7 +621,7 @@ struct FxNvfp4 {
 template <int LAYOUT>
 struct FxQ4K {
     static constexpr int FMT = TITAN_Q4_K, CHUNK_COLS = 128;
-    static constexpr bool HAS_MFMA = true, PIPE = true;
+    static constexpr bool HAS_MFMA = true, PIPE = true, LAST_CACHED = false;
     struct Off { uint32_t c, h; };
     struct Raw { uint32_t w[4]; uint4 hdr; };
     struct Dec { float ds[4], dm[4]; };  // [2*c4' + (0: low / 1: high)]
@@ -632,7 +632,7 @@ struct FxQ4K {
         else
             return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_q4k_hdr_off(g, row, 0)};
     }
-    template <int GS>
+    template <int GS, bool NT = true>
     TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
         const uint32_t blk = (uint32_t)c >> 1;
         if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
@@ -642,7 +642,7 @@ struct FxQ4K {
             for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (q + 16u * i));
         } else {
             r.hdr = ld_u128(w.codes + (o.h + blk * 256u));
-            uint4 q = ld_stream_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_codes_u128<NT>(w.codes + (o.c + (uint32_t)c * 1024u));
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
     }
@@ -804,10 +804,10 @@ struct FxQ3K {
         return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_q3k_hmask_off(g, row, 0, j),
                 (uint32_t)tiled_q3k_sc_off(g, row, 0), (uint32_t)tiled_q3k_d_off(g, row, 0)};
     }
-    template <int GS>
+    template <int GS, bool NT = true>
     TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
         const uint32_t b = (uint32_t)c;
-        uint4 q = ld_stream_u128(w.codes + (o.c + b * 1024u));
+        uint4 q = ld_codes_u128<NT>(w.codes + (o.c + b * 1024u));
         r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         const uint8_t* hp = w.codes + (o.h + b * 512u);
         r.hm0 = ld_u32(hp);
@@ -1013,13 +1013,13 @@ struct FxFp8 {
         else
             return {(uint32_t)tiled_code_off(w.g, row, 0, j)};
     }
-    template <int GS>
+    template <int GS, bool NT = true>
     TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
         if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
 #pragma unroll
             for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
         } else {
-            uint4 q = ld_stream_u128(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_codes_u128<NT>(w.codes + (o.c + (uint32_t)c * 1024u));
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
     }

@@ -31,6 +31,19 @@ template <class F>
 struct requires_sb_cell<F, std::void_t<decltype(F::SB_CELL)>> : std::true_type {};
 
 template <class F, class = void>
+struct has_last_cached : std::false_type {};
+template <class F>
+struct has_last_cached<F, std::void_t<decltype(F::LAST_CACHED)>> : std::true_type {};
+// Whether a wave loads its last weight group with cached loads (default) or,
+// like the others, nontemporal (LAST_CACHED = false: the branch between the
+// two measured slower than the refetch it saves)
+template <class F>
+constexpr bool last_cached() {
+    if constexpr (has_last_cached<F>::value) return F::LAST_CACHED;
+    else return true;
+}
+
+template <class F, class = void>
 struct has_sx_max_m : std::false_type {};
 template <class F>
 struct has_sx_max_m<F, std::void_t<decltype(F::SX_MAX_M)>> : std::true_type {};
@@ -275,11 +288,22 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     // a group is U consecutive chunks starting at a multiple of U.
     const int pspan = pchunks >> ks_log;
     auto chunk_at = [&](int ph, int g, int u) { return ph * pchunks + part * pspan + g * U + u; };
-    auto load_group = [&](int ph, int g, typename F::Raw (&R)[U]) {
+    // stream: nontemporal code loads.  For LAST_CACHED formats the wave's
+    // last group is loaded cached, so that the repeated loads past it (below)
+    // hit the cache instead of fetching the group from memory again.
+    auto load_group = [&](int ph, int g, typename F::Raw (&R)[U], bool stream) {
+        if (stream) {
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int cc = chunk_at(ph, g, u);
-            F::template load<GS>(W, off, cc < nchunks ? cc : 0, j, R[u]);
+            for (int u = 0; u < U; u++) {
+                const int cc = chunk_at(ph, g, u);
+                F::template load<GS, true>(W, off, cc < nchunks ? cc : 0, j, R[u]);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int cc = chunk_at(ph, g, u);
+                F::template load<GS, false>(W, off, cc < nchunks ? cc : 0, j, R[u]);
+            }
         }
         if constexpr (has_sb_cell<F>()) {
             static_assert(U % GS == 0, "a chunk group holds whole scale cells");
@@ -494,9 +518,10 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     static_assert(DEPTH == 2 || DEPTH == 3, "load depth");
     typename F::Raw rbuf[DEPTH][U];
     auto load_q = [&](int q, typename F::Raw (&R)[U]) {
+        const bool stream = !last_cached<F>() || q < ngroups - 1;
         q = q < ngroups ? q : ngroups - 1;
         const int p = q / gpp;
-        load_group(p, q - p * gpp, R);
+        load_group(p, q - p * gpp, R, stream);
     };
     auto fold_q = [&](int q, const typename F::Raw (&R)[U]) {
         const int p = q / gpp;
