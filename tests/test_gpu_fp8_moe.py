@@ -164,3 +164,43 @@ def test_fp8_gemm_full_size(M, N, K):
     rows = np.random.default_rng(0).choice(M, 8, replace=False)
     o8 = O.gemm_fp8(xq.cpu().numpy()[rows], sa.cpu().numpy()[rows], wq.cpu().numpy(), sw.cpu().numpy())
     assert_close_out(out.float().double().cpu().numpy()[rows], o8.astype(np.float64), "bf16")
+
+
+def e4m3_conversion_cases():
+    """fp32 values that pin an e4m3 conversion: every finite code value, every
+    midpoint between neighbours (ties to even) and the fp32 values one ulp
+    either side, the subnormal range, signed zeros, a NaN, random values."""
+    vals = O.e4m3_ref_table()
+    pos = np.unique(vals[np.isfinite(vals) & (vals >= 0) & (vals <= 448)])
+    mids = (pos[:-1].astype(np.float64) + pos[1:]) / 2
+    mids = mids.astype(np.float32)
+    up = np.nextafter(mids, np.float32(np.inf))
+    dn = np.nextafter(mids, np.float32(-np.inf))
+    rnd = np.random.default_rng(5).uniform(0, 448, 4000).astype(np.float32)
+    tiny = np.array([2.0 ** -10, 2.0 ** -10 * 1.0000001, 2.0 ** -11, 2.0 ** -30, 0.0], np.float32)
+    p = np.concatenate([pos, mids, up, dn, rnd, tiny]).astype(np.float32)
+    out = np.concatenate([p, -p, np.array([np.nan, -0.0], np.float32)])
+    return out[(out <= 448) | np.isnan(out)]
+
+
+def test_fp8_quantize_rows_conversion_exhaustive():
+    """titan_fp8_quantize_rows on fp32 rows whose largest magnitude is 448
+    (scale exactly 1): every other element is converted as it is, and must
+    give the oracle's RNE e4m3 code (fp4.cu-style saturation, NaN -> 0x7F)."""
+    v = e4m3_conversion_cases()
+    K = 1024
+    rows = -(-len(v) // (K - 1))
+    x = np.zeros((rows, K), np.float32)
+    flat = np.concatenate([v, np.zeros(rows * (K - 1) - len(v), np.float32)])
+    x[:, 1:] = flat.reshape(rows, K - 1)
+    x[:, 0] = 448.0
+    xd = torch.from_numpy(x).cuda()
+    xq = torch.empty(rows, K, dtype=torch.uint8, device="cuda")
+    xs = torch.empty(rows, dtype=torch.float32, device="cuda")
+    tq.fp8_quantize_rows(xd, xq, xs)
+    torch.cuda.synchronize()
+    assert np.all(xs.cpu().numpy() == 1.0)
+    want = O.f32_to_e4m3(x.reshape(-1)).reshape(rows, K)
+    got = xq.cpu().numpy()
+    bad = np.nonzero(got != want)
+    assert bad[0].size == 0, [(float(x[i, j]), int(got[i, j]), int(want[i, j])) for i, j in zip(*bad)][:10]

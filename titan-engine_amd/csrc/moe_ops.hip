@@ -224,11 +224,29 @@ __global__ __launch_bounds__(256) void fp8_quant_rows_vec_kernel(const void* __r
     const float sc = amax > 0.0f ? amax / 448.0f : 1.0f;
     if (tid == 0) xs[m] = sc;
     auto put8 = [&](int k, const float* v) {
+#ifndef TQ_FP8_SOFT_CVT
+        // hardware RNE conversion (v_cvt_pk_fp8_f32, OCP e4m3): |v / sc| <=
+        // 448 (1 + 2^-23) here, which rounds to at most 448, so no input
+        // reaches the saturating range.  The hardware writes NaN as 0xFF (no
+        // finite code); those bytes become 0x7F, the software conversion's NaN.
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) y[i] = v[i] / sc;
+        uint32_t lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+        lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], (int)lo, true);
+        uint32_t hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], 0, false);
+        hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], (int)hi, true);
+        auto nan_fix = [](uint32_t w) {  // bit 7 of every 0xFF byte cleared (no carries: bytes <= 0x80)
+            return w ^ (((w & 0x7F7F7F7Fu) + 0x01010101u) & w & 0x80808080u);
+        };
+        *(uint2*)(xq + base + k) = make_uint2(nan_fix(lo), nan_fix(hi));
+#else
         uint32_t q[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) q[i] = f32_to_e4m3_rne_sat(v[i] / sc);
         *(uint2*)(xq + base + k) = make_uint2(q[0] | q[1] << 8 | q[2] << 16 | q[3] << 24,
                                               q[4] | q[5] << 8 | q[6] << 16 | q[7] << 24);
+#endif
     };
     if (held) {
 #pragma unroll
