@@ -155,3 +155,48 @@ def test_cpp_shim_compiles_and_forwards(tmp_path):
                     "-L", libdir, "-ltitan_qmm", f"-Wl,-rpath,{libdir}", "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
     assert out == ["9", str(tq.ERR_INVALID_ARG)]
+
+
+def test_every_entry_point_rejects_bad_arguments():
+    """Null pointers and non-positive sizes return TITAN_ERR_INVALID_ARG before
+    any device work (so this runs without a GPU); the reference checks
+    nothing and returns void (dispatch.h:30-130)."""
+    import ctypes
+    L = tq.lib()
+    E = tq.ERR_INVALID_ARG
+    N = None
+    W = tq.QWeightC()
+    calls = {
+        "titan_dequant_matvec_int4": (N, N, N, N, N, 16, 128, 128, N),
+        "titan_dequant_matvec_int2": (N, N, N, N, N, 16, 128, 64, N),
+        "titan_dequant_matvec_fp4": (N, N, N, N, 16, 128, 32, N),
+        "titan_dequant_matvec_nvfp4": (N, N, ctypes.c_float(1.0), N, N, 16, 128, N),
+        "titan_sparse_dequant_matvec_int4": (N, N, N, N, N, N, 1, 128, 128, N),
+        "titan_quantize_fp4": (N, N, N, 128, 32, N),
+        "titan_qgemm": (N, N, tq.FP16, 128, N, tq.FP16, 16, 1, N),
+        "titan_qgemm_batched": (ctypes.byref(W), N, N, 0, tq.FP16, tq.FP16, 1, N),
+        "titan_qdequant": (N, N, tq.FP32, N),
+        "titan_fp8_quantize_rows": (N, tq.BF16, 1, 128, N, N, N),
+        "titan_fp8_gemm": (N, N, N, N, N, tq.BF16, 128, 128, 128, N),
+        "titan_moe_gate": (N, N, N, 128, 8, N),
+        "titan_moe_topk": (N, N, N, 8, 2, N),
+        "titan_moe_topk_batched": (N, N, N, 1, 8, 2, N),
+        "titan_swiglu": (N, N, N, 16, N),
+        "titan_fused_moe_combine_norm": (N, N, N, N, N, ctypes.c_float(0.0), N, 16, 1,
+                                         ctypes.c_float(1e-6), N),
+        "titan_moe_nvfp4_forward": (N, 8, 512, 512, N, tq.BF16, 1, N, N, 2, N, N,
+                                    ctypes.c_float(0.0), N, tq.BF16, N, ctypes.c_size_t(0), N),
+        "titan_gemv_bf16_to_fp32": (N, N, N, 16, 16, N),
+        "titan_gemv_fp32": (N, N, N, 16, 16, N),
+        "titan_gemv_fp32_batched": (N, N, N, 16, 16, 2, N),
+        "titan_matvec_dispatch": (N, N, N, N),
+    }
+    for name, args in calls.items():
+        assert getattr(L, name)(*args) == E, name
+    # sizes: zero or negative rows / cols / tokens
+    x = (ctypes.c_uint8 * 64)()
+    p = ctypes.cast(x, ctypes.c_void_p)
+    assert L.titan_gemv_fp32(p, p, p, 0, 16, N) == E
+    assert L.titan_gemv_fp32(p, p, p, 16, -1, N) == E
+    assert L.titan_fp8_quantize_rows(p, tq.BF16, 0, 128, p, p, N) == E
+    assert L.titan_swiglu(p, p, p, 0, N) == E
