@@ -167,7 +167,7 @@ def bench_kquant(fmt, n, k, M, gen, steps, warmup):
     algo = dev.numel() + M * k * 2 + M * n * 2
     ms, gbs = bench_single(Wl, x, y, steps, warmup, algo)
     del Wl, dev
-    return dict(ms=ms, gbs=gbs, bytes=algo)
+    return dict(ms=ms, gbs=gbs, bytes=algo, ref=(blk, None, None))
 
 
 def bench_kquant_layer(fmt, M, gen, steps, warmup):
@@ -204,7 +204,11 @@ def bench_int2(n, k, M, gen, steps, warmup):
     y = torch.empty(M, n, device="cuda", dtype=torch.float16)
     algo = m["tiled"].numel() + M * k * 2 + M * n * 2
     ms, gbs = bench_single(Wl, x, y, steps, warmup, algo)
-    return dict(ms=ms, gbs=gbs, bytes=algo)
+    import numpy as np
+    w, s, b = m["ref"]
+    ref = (w.cpu().numpy().view(np.uint32), s.cpu().numpy().view(np.uint16),
+           b.cpu().numpy().view(np.uint16))
+    return dict(ms=ms, gbs=gbs, bytes=algo, ref=ref)
 
 
 def bench_fp8(M, N, K, gen, steps, warmup):
@@ -226,7 +230,9 @@ def bench_fp8(M, N, K, gen, steps, warmup):
     ms = time_launches(step, steps, warmup)
     gemm_ms = time_launches(lambda i: tq.fp8_gemm(xq, xs, wq, sw, out), steps, warmup)
     fl = 2.0 * M * N * K
-    return dict(ms=ms, tflops=fl / ms / 1e9, gemm_ms=gemm_ms, gemm_tflops=fl / gemm_ms / 1e9)
+    host = (xq[:4].cpu().numpy(), xs[:4].cpu().numpy(), wq.cpu().numpy(), sw.cpu().numpy())
+    return dict(ms=ms, tflops=fl / ms / 1e9, gemm_ms=gemm_ms, gemm_tflops=fl / gemm_ms / 1e9,
+                host=host)
 
 
 NV_EXPERT_BYTES = 3 * (2048 * 7168 // 2 + 2048 * 7168 // 16 + 4)  # codes + e4m3 + global
@@ -277,11 +283,13 @@ def bench_moe(T, steps, warmup, gen, experts=None):
         tq.moe_nvfp4_forward(table, E, hidden, inter, x, idx, w, out, ws)
 
     ms = time_launches(step, steps, warmup)
+    torch.cuda.synchronize()
+    route = (idx.cpu().numpy(), w.cpu().numpy(), x.float().cpu().numpy())
     used = int(torch.unique(idx).numel())
     nbytes = used * NV_EXPERT_BYTES + T * hidden * 2 * 2 + T * E * 4
     flops = 2.0 * T * k * 3 * inter * hidden
     return dict(ms=ms, experts_hit=used, bytes=nbytes, gbs=nbytes / ms / 1e6,
-                tflops=flops / ms / 1e9), (mats, table)
+                tflops=flops / ms / 1e9, route=route), (mats, table)
 
 
 # ---------------------------------------------------------------- CPU baseline
@@ -330,6 +338,95 @@ def cpu_baseline(layer, budget_s=12.0):
     mt = dict(value=round(nbytes * mt_passes / el / 1e9, 3), unit="GB/s", cores=nth, kind="port",
               sample=f"{mt_passes} pass(es), rows partitioned over {nth} pthreads")
     return res, mt
+
+
+def cpu_time(fn, budget_s, max_passes=1000):
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or passes >= max_passes:
+            return passes, el
+
+
+def cpu_gemv_baseline(fmt, ref, g, gs, rows, cols, nbytes, budget_s=1.0):
+    """The matmul_avx.cpp:54-100 loop shape (row-serial, column-ascending,
+    one fp32 accumulator) restated for `fmt` by the oracle, one thread: the
+    reference has no CPU routine for Q4_K / Q3_K / INT2."""
+    import numpy as np
+    from oracle import oracle_ctypes as O
+    codes, sc, bi = ref
+    x = np.random.default_rng(1).normal(0, 1, cols).astype(np.float32)
+    passes, el = cpu_time(lambda: O.matvec_fmt_mt(fmt, codes, sc, bi, g, gs, x, rows, cols, 1),
+                          budget_s)
+    return dict(value=round(nbytes * passes / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                sample=f"{passes} pass(es) of the {rows}x{cols} {fmt} GEMV, M=1 fp32 x, "
+                       f"{el:.2f} s, oracle restatement of the matmul_avx.cpp loop")
+
+
+def cpu_moe_baseline(mats, route, hidden, inter, budget_s=2.0):
+    """C4 on the host: per token, its k experts in parallel threads, one
+    thread per expert (execute_experts_parallel, expert_cpu.cpp:39-102), each
+    gate / up / SwiGLU / down with the oracle's NVFP4 GEMV (fp4.cu:187-238
+    loop order); weights read back from the GPU's TILED buffers and unpacked."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+    import titan_qmm as tq
+    from oracle import oracle_ctypes as O
+    idx, wts, x = route
+    k = idx.shape[1]
+    cache = {}
+
+    def ref_of(e):
+        if e not in cache:
+            parts = []
+            for t, (n, kk) in zip(mats[e], ((inter, hidden), (inter, hidden), (hidden, inter))):
+                c, s, _ = tq.unpack_host(tq.NVFP4, n, kk, t.cpu().numpy(),
+                                         np.zeros((n, kk // 2), np.uint8),
+                                         np.zeros((n, kk // 16), np.uint8))
+                parts.append((c, s, n, kk))
+            cache[e] = parts
+        return cache[e]
+
+    g = 0.02 / 448
+    toks = 0
+
+    def expert(e, xt):
+        (cg, sg, n, kk), (cu, su, _, _), (cd, sd, nd, kd) = ref_of(e)
+        a = O.matvec_nvfp4(cg, sg, g, xt, n, kk)
+        u = O.matvec_nvfp4(cu, su, g, xt, n, kk)
+        h = (a / (1.0 + np.exp(-a)) * u).astype(np.float32)
+        return O.matvec_nvfp4(cd, sd, g, h, nd, kd)
+
+    for e in set(idx[:4].reshape(-1).tolist()):
+        ref_of(e)  # unpack outside the timed region
+    with ThreadPoolExecutor(max_workers=k) as pool:
+        t0 = time.perf_counter()
+        while True:
+            t = toks % min(4, idx.shape[0])
+            ys = list(pool.map(lambda j: expert(int(idx[t, j]), x[t]), range(k)))
+            _ = sum(wts[t, j] * ys[j] for j in range(k))
+            toks += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+    nbytes = toks * k * NV_EXPERT_BYTES
+    return dict(value=round(nbytes / el / 1e9, 3), unit="GB/s", cores=k, kind="port",
+                ms_per_token=round(1e3 * el / toks, 1),
+                sample=f"{toks} token(s), {k} experts each on {k} threads, {el:.2f} s")
+
+
+def cpu_fp8_baseline(host, N, K, budget_s=1.0):
+    """The oracle's scalar FP8 GEMM (e4m3 x e4m3, fp32 accumulate, per-token
+    and per-channel scales) on a sample of activation rows, one thread; the
+    reference has no FP8 CPU path."""
+    from oracle import oracle_ctypes as O
+    A, sa, W, sw = host
+    rows = 1
+    passes, el = cpu_time(lambda: O.gemm_fp8(A[:rows], sa[:rows], W, sw), budget_s, max_passes=50)
+    return dict(value=round(2.0 * rows * N * K * passes / el / 1e12, 6), unit="TFLOP/s", cores=1,
+                kind="port", sample=f"{passes} pass(es) of {rows} activation row x {N}x{K}, {el:.2f} s")
 
 
 def cpu_model():
@@ -420,6 +517,9 @@ def main():
         secondary.append(dict(config="Q4_K 4096x4096 GEMV (synthetic codes)", M=1,
                               ms=round(r["ms"], 5), GBps=round(r["gbs"], 1),
                               frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4)))
+        if not args.no_cpu:
+            secondary[-1]["cpu_baseline"] = cpu_gemv_baseline("q4k", r["ref"], 0.0, 0, 4096, 4096,
+                                                              r["bytes"])
         for M in (1, 4):
             for n, k in LLAMA70B:
                 log(f"Q3_K / INT2 {n}x{k} M={M}")
@@ -427,10 +527,16 @@ def main():
                 secondary.append(dict(config=f"Q3_K {n}x{k} GEMV (synthetic codes)", M=M,
                                       ms=round(r["ms"], 5), GBps=round(r["gbs"], 1),
                                       frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4)))
+                if M == 1 and not args.no_cpu:
+                    secondary[-1]["cpu_baseline"] = cpu_gemv_baseline("q3k", r["ref"], 0.0, 0, n, k,
+                                                                      r["bytes"], budget_s=0.5)
                 r = bench_int2(n, k, M, gen, max(20, K // 2), 5)
                 secondary.append(dict(config=f"INT2 g64 {n}x{k} GEMV", M=M, ms=round(r["ms"], 5),
                                       GBps=round(r["gbs"], 1),
                                       frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4)))
+                if M == 1 and not args.no_cpu:
+                    secondary[-1]["cpu_baseline"] = cpu_gemv_baseline("int2", r["ref"], 0.0, 64, n, k,
+                                                                      r["bytes"], budget_s=0.5)
                 torch.cuda.empty_cache()
         ex = None
         for T in (64, 1024):
@@ -441,6 +547,9 @@ def main():
                                   experts_hit=r["experts_hit"], GBps=round(r["gbs"], 1),
                                   frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4),
                                   TFLOPS=round(r["tflops"], 1)))
+            if T == 64 and not args.no_cpu:
+                log("NVFP4 MoE CPU baseline")
+                secondary[-1]["cpu_baseline"] = cpu_moe_baseline(ex[0], r["route"], 7168, 2048)
         del ex
         torch.cuda.empty_cache()
         for (M, N, Kd) in [(2048, 14336, 4096), (2048, 4096, 14336)]:
@@ -450,6 +559,8 @@ def main():
                                   ms=round(r["ms"], 4), TFLOPS=round(r["tflops"], 1),
                                   gemm_only_TFLOPS=round(r["gemm_tflops"], 1),
                                   frac_fp8_peak=round(r["gemm_tflops"] / FP8_PEAK_TFLOPS, 4)))
+            if not args.no_cpu:
+                secondary[-1]["cpu_baseline"] = cpu_fp8_baseline(r["host"], N, Kd)
 
     cpu, cpu_mt = (None, None)
     if not args.no_cpu:
