@@ -477,6 +477,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--headline-only", action="store_true")
+    ap.add_argument("--fp8-only", action="store_true",
+                    help="only the two FP8 prefill GEMMs (for counter runs); prints their lines")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM byte-counter calibration)")
@@ -494,6 +496,15 @@ def main():
     tq.lib()
     gen = torch.Generator(device="cuda").manual_seed(0)
     K, W = args.steps, args.warmup
+
+    if args.fp8_only:
+        lines = []
+        for (M, N, Kd) in [(2048, 14336, 4096), (2048, 4096, 14336)]:
+            r = bench_fp8(M, N, Kd, gen, K, W)
+            lines.append(dict(config=f"FP8 E4M3 GEMM M={M} N={N} K={Kd}", ms=round(r["ms"], 4),
+                              gemm_only_TFLOPS=round(r["gemm_tflops"], 1)))
+        print(json.dumps(lines))
+        return
 
     log("headline: INT4 g128 Llama-3-8B layer, M=1")
     h = bench_int4_layer(1, K, W, gen)
