@@ -131,6 +131,27 @@ int titan_qgemm(const titan_qweight* W, const void* X, int x_dtype, int64_t ldx,
 int titan_qgemm_batched(const titan_qweight* Ws, const void* const* Xs, void* const* Ys,
                         int n, int x_dtype, int y_dtype, int M, hipStream_t stream);
 
+/* The same products with the K (column) range of small problems split across
+ * workgroups (no counterpart in the reference: its GEMV launches one block
+ * per row, dequant.cu:227-240).  Used for the 256-column-chunk formats
+ * (INT2, Q3_K) when the launch would otherwise hold fewer waves than the
+ * chip needs (e.g. the 1024 x 8192 projections of a 70B layer), where it
+ * measured faster; every other case runs exactly as titan_qgemm /
+ * titan_qgemm_batched.
+ * `workspace` is a caller-owned device buffer of at least
+ * titan_qgemm_workspace_bytes() bytes, 256-byte aligned, zero-filled once
+ * before its first use; every call leaves its counters at zero again, so it
+ * can be reused by later calls ordered after it on a stream.  Calls that
+ * share one workspace must not overlap.  Results are deterministic (the
+ * partial sums are added in a fixed order). */
+size_t titan_qgemm_workspace_bytes(const int* rows, int n, int M);
+int titan_qgemm_ws(const titan_qweight* W, const void* X, int x_dtype, int64_t ldx,
+                   void* Y, int y_dtype, int64_t ldy, int M, void* workspace,
+                   size_t workspace_bytes, hipStream_t stream);
+int titan_qgemm_batched_ws(const titan_qweight* Ws, const void* const* Xs, void* const* Ys,
+                           int n, int x_dtype, int y_dtype, int M, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream);
+
 /* Exact dequantization: out[r][c] (out_dtype FP32 is bit-exact with the
  * reference's dequantized value; FP16/BF16 round it to nearest-even). */
 int titan_qdequant(const titan_qweight* W, void* out, int out_dtype, hipStream_t stream);

@@ -60,6 +60,22 @@ def test_qgemm_parity(fmt, lay, M, rng):
         assert_close_out(to_np(y), ref, ydt)
 
 
+@pytest.mark.parametrize("fmt,lay", [("int2", "ref"), ("int2", "tiled"), ("q3k", "tiled"),
+                                     ("q4k", "tiled"), ("int4", "ref")])
+@pytest.mark.parametrize("M", [17, 32, 40])
+def test_qgemm_many_tokens(fmt, lay, M, rng):
+    """More than 16 fp16 tokens on the matrix-core GEMV: 256-column-chunk
+    formats (INT2, Q3_K) take 16 tokens a launch (the activation stage of 32
+    would not fit in LDS), the others 32."""
+    rows, cols, gs = SHAPES[fmt]
+    d = make_weights(fmt, rows, cols, rng, gs=gs or 128)
+    W = upload(d, LAYOUTS[lay])
+    x, x64 = act(M, cols, "f16", rng)
+    y = tq.qgemm(W, x, out_dtype=torch.float16)
+    torch.cuda.synchronize()
+    assert_close_out(to_np(y), x64 @ d["deq"].astype(np.float64).T, "f16")
+
+
 @pytest.mark.parametrize("fmt", ["int4", "int2", "fp4", "nvfp4", "q4k", "fp8"])
 def test_ragged_rows_and_strides(fmt, rng):
     # rows not a multiple of 16; x / y with padded row strides

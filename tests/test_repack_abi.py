@@ -175,6 +175,9 @@ def test_every_entry_point_rejects_bad_arguments():
         "titan_quantize_fp4": (N, N, N, 128, 32, N),
         "titan_qgemm": (N, N, tq.FP16, 128, N, tq.FP16, 16, 1, N),
         "titan_qgemm_batched": (ctypes.byref(W), N, N, 0, tq.FP16, tq.FP16, 1, N),
+        "titan_qgemm_ws": (N, N, tq.FP16, 128, N, tq.FP16, 16, 1, N, ctypes.c_size_t(0), N),
+        "titan_qgemm_batched_ws": (ctypes.byref(W), N, N, 0, tq.FP16, tq.FP16, 1, N,
+                                   ctypes.c_size_t(0), N),
         "titan_qdequant": (N, N, tq.FP32, N),
         "titan_fp8_quantize_rows": (N, tq.BF16, 1, 128, N, N, N),
         "titan_fp8_gemm": (N, N, N, N, N, tq.BF16, 128, 128, 128, N),
@@ -200,3 +203,11 @@ def test_every_entry_point_rejects_bad_arguments():
     assert L.titan_gemv_fp32(p, p, p, 16, -1, N) == E
     assert L.titan_fp8_quantize_rows(p, tq.BF16, 0, 128, p, p, N) == E
     assert L.titan_swiglu(p, p, p, 0, N) == E
+    # K-split workspace: one counter region per problem, 16 parts of partials
+    rows = (ctypes.c_int * 2)(4096, 1000)
+    one = L.titan_qgemm_workspace_bytes(rows, 1, 1)
+    assert one == 16 * 4096 * 4 + 1024
+    assert L.titan_qgemm_workspace_bytes(rows, 2, 1) == one + (16 * 1008 * 4 + 252 + 255) // 256 * 256
+    assert L.titan_qgemm_workspace_bytes(rows, 1, 64) == 32 * one - 31 * 1024
+    assert L.titan_qgemm_workspace_bytes(rows, 0, 1) == 0
+    assert L.titan_qgemm_workspace_bytes(N, 1, 1) == 0

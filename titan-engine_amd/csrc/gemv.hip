@@ -97,7 +97,7 @@ int chunk_cols_of(int fmt) { return 512 / code_bits(fmt); }
 // at most 8 tokens.
 int run_gemv(const titan_qweight* Ws, const void* const* Xs, const int64_t* ldx,
              void* const* Ys, const int64_t* ldy, int n, int xdt, int ydt, int M,
-             hipStream_t st) {
+             hipStream_t st, void* ws = nullptr, size_t ws_bytes = 0) {
     if (n <= 0 || n > TITAN_MAX_BATCH || M <= 0) return TITAN_ERR_INVALID_ARG;
     if (!tqh::act_dtype_ok(xdt) || !tqh::act_dtype_ok(ydt)) return TITAN_ERR_INVALID_ARG;
     bool fast = true;
@@ -113,6 +113,8 @@ int run_gemv(const titan_qweight* Ws, const void* const* Xs, const int64_t* ldx,
     a.n = n;
     a.xdt = xdt;
     a.ydt = ydt;
+    a.ws = ws;
+    a.ws_bytes = ws_bytes;
     int total_tiles = 0;
     bool f16 = xdt == TITAN_FP16;
     for (int i = 0; i < n; i++) {
@@ -169,13 +171,15 @@ int run_gemv(const titan_qweight* Ws, const void* const* Xs, const int64_t* ldx,
     for (int i = 1; i < n; i++)
         if (a.p[i].gsteps != a.p[0].gsteps) {
             for (int q = 0; q < n; q++) {
-                int s = run_gemv(&Ws[q], &Xs[q], &ldx[q], &Ys[q], &ldy[q], 1, xdt, ydt, M, st);
+                int s = run_gemv(&Ws[q], &Xs[q], &ldx[q], &Ys[q], &ldy[q], 1, xdt, ydt, M, st, ws, ws_bytes);
                 if (s) return s;
             }
             return TITAN_OK;
         }
     const int mode = !f16 ? kModeF32 : (has_mfma ? kModeMfma : kModeDot2);
-    const int per_launch = mode == kModeMfma ? 32 : 8;
+    // MFMA: up to 32 tokens a launch; 256-column chunks (INT2, Q3_K) stage
+    // twice the columns per round, so 16 (32 would need 256 KiB of LDS)
+    const int per_launch = mode != kModeMfma ? 8 : chunk_cols_of(fmt) > 128 ? 16 : 32;
     for (int m0 = 0; m0 < M; m0 += per_launch) {
         a.m0 = m0;
         int mc = M - m0 < per_launch ? M - m0 : per_launch;
@@ -215,6 +219,54 @@ extern "C" int titan_qgemm_batched(const titan_qweight* Ws, const void* const* X
         ldy[i] = Ws[i].rows;
     }
     return run_gemv(Ws, Xs, ldx, Ys, ldy, n, x_dtype, y_dtype, M, stream);
+}
+
+// ---- K split across workgroups (caller workspace) ---------------------------
+extern "C" size_t titan_qgemm_workspace_bytes(const int* rows, int n, int M) {
+    if (!rows || n <= 0 || n > TITAN_MAX_BATCH || M <= 0) return 0;
+    const int m = M < 32 ? M : 32;  // tokens per launch at most
+    size_t b = 0;
+    for (int i = 0; i < n; i++) {
+        if (rows[i] <= 0) return 0;
+        b += gemv_xs_bytes(rows[i], m);
+    }
+    return b;
+}
+
+static int ws_check(const titan_qweight* Ws, int n, int M, const void* ws, size_t ws_bytes) {
+    if (!ws || ((uintptr_t)ws & 255)) return TITAN_ERR_INVALID_ARG;
+    int rows[TITAN_MAX_BATCH];
+    for (int i = 0; i < n; i++) rows[i] = Ws[i].rows;
+    const size_t need = titan_qgemm_workspace_bytes(rows, n, M);
+    return need == 0 ? TITAN_ERR_INVALID_ARG : (ws_bytes < need ? TITAN_ERR_WORKSPACE : TITAN_OK);
+}
+
+extern "C" int titan_qgemm_ws(const titan_qweight* W, const void* X, int x_dtype, int64_t ldx,
+                              void* Y, int y_dtype, int64_t ldy, int M, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream) {
+    if (!W || M <= 0 || W->rows <= 0) return TITAN_ERR_INVALID_ARG;
+    if (int s = ws_check(W, 1, M, workspace, workspace_bytes)) return s;
+    const void* xs[1] = {X};
+    void* ys[1] = {Y};
+    return run_gemv(W, xs, &ldx, ys, &ldy, 1, x_dtype, y_dtype, M, stream, workspace,
+                    workspace_bytes);
+}
+
+extern "C" int titan_qgemm_batched_ws(const titan_qweight* Ws, const void* const* Xs,
+                                      void* const* Ys, int n, int x_dtype, int y_dtype, int M,
+                                      void* workspace, size_t workspace_bytes,
+                                      hipStream_t stream) {
+    if (!Ws || !Xs || !Ys || n <= 0 || n > TITAN_MAX_BATCH || M <= 0) return TITAN_ERR_INVALID_ARG;
+    for (int i = 0; i < n; i++)
+        if (Ws[i].rows <= 0) return TITAN_ERR_INVALID_ARG;
+    if (int s = ws_check(Ws, n, M, workspace, workspace_bytes)) return s;
+    int64_t ldx[TITAN_MAX_BATCH], ldy[TITAN_MAX_BATCH];
+    for (int i = 0; i < n; i++) {
+        ldx[i] = Ws[i].cols;
+        ldy[i] = Ws[i].rows;
+    }
+    return run_gemv(Ws, Xs, ldx, Ys, ldy, n, x_dtype, y_dtype, M, stream, workspace,
+                    workspace_bytes);
 }
 
 extern "C" int titan_qdequant(const titan_qweight* W, void* out, int out_dtype,

@@ -96,6 +96,15 @@ struct GemvProb {
     int ntiles;    // ceil(rows / 16)
     int gsteps;    // MFMA word steps per scale group (power of two <= 4)
     int ks_log;    // log2 of the waves sharing one row tile (K split)
+    // K split across workgroups (xs_log > 0 only with a caller workspace):
+    // 2^xs_log consecutive workgroups take equal contiguous chunk ranges of
+    // the same row tiles, write fp32 partials to wsp[part][token][row]
+    // (row stride rpad) and the last to arrive (counter wsc[tile group])
+    // adds them in part order and stores the outputs.
+    int xs_log;
+    int rpad;
+    float* wsp;
+    int* wsc;
 };
 
 struct GemvArgs {
@@ -105,7 +114,27 @@ struct GemvArgs {
     int m0;      // first token of this launch
     int mcount;  // tokens in this launch (<= the kernel's template width)
     int pc;      // staged columns per phase (whole groups of chunks)
+    // host only: caller workspace for the cross-workgroup K split (null: none)
+    void* ws;
+    size_t ws_bytes;
 };
+
+#ifndef TQ_GEMV_XS_WAVES
+#define TQ_GEMV_XS_WAVES 2048  // waves the cross-workgroup split aims for
+#endif
+#ifndef TQ_GEMV_XS_MAX_LOG
+#define TQ_GEMV_XS_MAX_LOG 4   // at most 16 workgroups share a row tile
+#endif
+
+// Workspace of the cross-workgroup K split.  Every problem's counters (one
+// int per row tile, 256-byte rounded) come first, at offsets that do not
+// depend on the token count, so that launches with different token counts
+// can share one workspace; the partials [16][m][rpad] fp32 follow.
+inline size_t gemv_xs_cnt_bytes(int rows) { return ((size_t)(rows + 15) / 16 * 4 + 255) / 256 * 256; }
+inline size_t gemv_xs_part_bytes(int rows, int m) {
+    return (size_t)m * ((size_t)(rows + 15) / 16 * 16) * 4 << TQ_GEMV_XS_MAX_LOG;
+}
+inline size_t gemv_xs_bytes(int rows, int m) { return gemv_xs_cnt_bytes(rows) + gemv_xs_part_bytes(rows, m); }
 
 // fp32 activations in column order plus fp32 sums of every 16 columns.
 template <int M>
@@ -240,7 +269,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
         if (bid >= a.p[i].wg_begin) pi = i;
     const GemvProb& P = a.p[pi];
     const WDesc& W = P.w;
-    const int rows = W.g.rows, nchunks = P.nchunks;
+    const int rows = W.g.rows;
 
     // the wave index is uniform: keep the chunk bookkeeping in scalar registers
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -248,8 +277,15 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     // KS waves share one row tile and split its chunks (part, part + KS, ...)
     const int ks_log = P.ks_log, KS = 1 << ks_log;
     const int part = wave & (KS - 1);
-    const int tile = (bid - P.wg_begin) * (kGemvWaves >> ks_log) + (wave >> ks_log);
+    const int xs_log = P.xs_log, XS = 1 << xs_log;
+    const int wgl = bid - P.wg_begin, xpart = wgl & (XS - 1), wgt = wgl >> xs_log;
+    const int tile = wgt * (kGemvWaves >> ks_log) + (wave >> ks_log);
     const int pc = a.pc;
+    // this workgroup's chunk range [c0, c0 + nchunks); chunk indices below
+    // are relative to c0
+    const int nchunks = P.nchunks >> xs_log;
+    const int c0 = xpart * nchunks;
+    const int colend = XS == 1 ? W.g.cols : (c0 + nchunks) * F::CHUNK_COLS;
 
     float* xf = lds;
     _Float16* xh = (_Float16*)lds;
@@ -296,13 +332,13 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int cc = chunk_at(ph, g, u);
-                F::template load<GS, true>(W, off, cc < nchunks ? cc : 0, j, R[u]);
+                F::template load<GS, true>(W, off, c0 + (cc < nchunks ? cc : 0), j, R[u]);
             }
         } else {
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int cc = chunk_at(ph, g, u);
-                F::template load<GS, false>(W, off, cc < nchunks ? cc : 0, j, R[u]);
+                F::template load<GS, false>(W, off, c0 + (cc < nchunks ? cc : 0), j, R[u]);
             }
         }
         if constexpr (has_sb_cell<F>()) {
@@ -310,7 +346,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int u = 0; u < U; u += GS) {
                 const int cc = chunk_at(ph, g, u);
-                F::template load_cell<GS>(W, off, cc < nchunks ? cc : 0, R[u]);
+                F::template load_cell<GS>(W, off, c0 + (cc < nchunks ? cc : 0), R[u]);
             }
         }
     };
@@ -325,8 +361,8 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     constexpr bool ONE = MODE != kModeF32 && (stage_local<F>() || M == 1);
     constexpr bool PERM = !stage_local<F>();
     auto phase_cols = [&](int ph, int& col0, int& ncols) {
-        col0 = ph * pchunks * F::CHUNK_COLS;
-        ncols = min(pchunks * F::CHUNK_COLS, W.g.cols - col0);
+        col0 = (c0 + ph * pchunks) * F::CHUNK_COLS;
+        ncols = min(pchunks * F::CHUNK_COLS, colend - col0);
     };
     auto stage_issue = [&](int ph, int round, auto& S) {
         constexpr int NI = sizeof(S.v) / sizeof(uint4);
@@ -423,8 +459,8 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
                 __syncthreads();
             }
         } else if (g == 0) {  // first group of a phase: stage its activations
-            const int col0 = ph * pchunks * F::CHUNK_COLS;
-            const int ncols = min(pchunks * F::CHUNK_COLS, W.g.cols - col0);
+            const int col0 = (c0 + ph * pchunks) * F::CHUNK_COLS;
+            const int ncols = min(pchunks * F::CHUNK_COLS, colend - col0);
             __syncthreads();
             if constexpr (MODE == kModeF32)
                 stage_f32<M>(xf, s16, pc, P.x, a.xdt, P.ldx, a.m0, a.mcount, col0, ncols, tid);
@@ -469,7 +505,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
 #pragma unroll
                     for (int n = 0; n < NB; n++) xu[n] = xt[n] + lbase;
                     F::template issue<NB, GS, SX>(R[u], j, xu, T1);
-                    const typename F::Dec dec = decode_u<F, GS>(W, R, u, cc, j);
+                    const typename F::Dec dec = decode_u<F, GS>(W, R, u, c0 + cc, j);
                     fold_into(T1, dec, cc, lbase);
                 }
             } else {
@@ -486,7 +522,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
                 }
                 if (u > 0) {
                     const int cp = chunk_at(ph, g, u - 1);
-                    const typename F::Dec dec = decode_u<F, GS>(W, R, u - 1, cp, j);
+                    const typename F::Dec dec = decode_u<F, GS>(W, R, u - 1, c0 + cp, j);
                     fold_into(T[(u - 1) & 1], dec, cp, lbase_of(cp));
                 }
             }
@@ -497,7 +533,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
                 const int cc = chunk_at(ph, g, u);
                 if (cc >= nchunks) continue;  // uniform per wave
                 const int lbase = (cc - ph * pchunks) * F::CHUNK_COLS;
-                const typename F::Dec dec = decode_u<F, GS>(W, R, u, cc, j);
+                const typename F::Dec dec = decode_u<F, GS>(W, R, u, c0 + cc, j);
 #pragma unroll
                 for (int m = 0; m < M; m++) {
                     if constexpr (MODE == kModeF32)
@@ -606,6 +642,57 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             }
         }
     }
+    if (XS > 1) {
+        // K split across workgroups: publish this part's sums; the last of
+        // the XS workgroups of the tile group adds the parts in order
+        // (deterministic) and stores.  Every workspace access is an
+        // agent-scope atomic (exchange, fetch-add, load), coherent across the
+        // XCDs without the write-back and invalidation of their whole L2
+        // caches that agent-scope fences cost (measured 4x slower); a part's
+        // exchanges have returned (their results are consumed) before its
+        // counter increment is issued.
+        __shared__ unsigned last_wg, sink;
+        unsigned got = 0;
+        if (part == 0 && row < rows) {
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const bool mine = MODE == kModeMfma ? (m >> 2) % 4 == j : j == 0;
+                if (mine && m < a.mcount)
+                    got ^= __hip_atomic_exchange((unsigned*)P.wsp + ((int64_t)xpart * a.mcount + m) * P.rpad + row,
+                                                 __float_as_uint(res[m]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        if (got == 0x7FC00001u) sink = got;  // keeps the exchanges' results live
+        __syncthreads();
+        if (tid == 0) {
+            const int old = __hip_atomic_fetch_add(P.wsc + wgt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_wg = old == XS - 1;
+            // the counter goes back to zero for the next call on this workspace
+            if (old == XS - 1) __hip_atomic_exchange(P.wsc + wgt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last_wg) return;
+        if (part == 0 && row < rows) {
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const bool mine = MODE == kModeMfma ? (m >> 2) % 4 == j : j == 0;
+                if (mine && m < a.mcount) {
+                    // every part's load is issued before the first is used
+                    constexpr int XMAX = 1 << TQ_GEMV_XS_MAX_LOG;
+                    unsigned pv[XMAX];
+#pragma unroll
+                    for (int x = 0; x < XMAX; x++)
+                        pv[x] = x < XS ? __hip_atomic_load((unsigned*)P.wsp + ((int64_t)x * a.mcount + m) * P.rpad + row,
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                       : 0u;
+                    float v = 0.0f;
+#pragma unroll
+                    for (int x = 0; x < XMAX; x++) v += __uint_as_float(pv[x]);
+                    res[m] = v;
+                }
+            }
+        }
+    }
     if (part == 0 && row < rows) {
 #pragma unroll
         for (int m = 0; m < M; m++) {
@@ -701,13 +788,59 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
         int ks = 0;
         while (ks < TQ_GEMV_KS_MAX && a.p[i].nchunks > target << ks) ks++;
         a.p[i].ks_log = ks;
+        a.p[i].xs_log = 0;
+    }
+    // Few waves (small matrices): with a caller workspace, split K across
+    // workgroups too.  Each wave keeps at least one whole group of U chunks;
+    // the problems' waves keep one workgroup per row tile group within the K
+    // split (ks = 0: four row tiles a workgroup, the smallest activation stage).
+    // Measured (rocprof, 1024 x 8192): Q3_K M = 1 11.2 -> 10.0 us, INT2 M = 4
+    // 13.8 -> 11.7 us; for the 128-column-chunk formats (INT4, Q4_K 4096^2:
+    // 8.2 -> 10.2 us) the partials' round trips cost more than the extra
+    // waves gain, so they keep the single-workgroup tiles.
+    if (a.ws && F::CHUNK_COLS > 128) {
+        constexpr int U = gemv_u<F, M, MODE>();
+        long long waves = 0;
+        for (int i = 0; i < a.n; i++) waves += (long long)a.p[i].ntiles << a.p[i].ks_log;
+        if (waves < TQ_GEMV_XS_WAVES) {
+            int xs = 0;
+            long long w0 = 0;
+            for (int i = 0; i < a.n; i++) w0 += a.p[i].ntiles;
+            auto fits = [&](int x) {
+                for (int i = 0; i < a.n; i++)
+                    if ((a.p[i].nchunks >> x) < U || (a.p[i].nchunks % (U << x)) != 0) return false;
+                return true;
+            };
+            while (xs < TQ_GEMV_XS_MAX_LOG && (w0 << xs) < TQ_GEMV_XS_WAVES && fits(xs + 1)) xs++;
+            size_t need = 0;
+            for (int i = 0; i < a.n; i++) need += gemv_xs_bytes(a.p[i].w.g.rows, a.mcount);
+            if (xs > 0 && (w0 << xs) > waves && need <= a.ws_bytes) {
+                char* cnt = (char*)a.ws;
+                for (int i = 0; i < a.n; i++) {
+                    a.p[i].wsc = (int*)cnt;
+                    cnt += gemv_xs_cnt_bytes(a.p[i].w.g.rows);
+                }
+                char* part = cnt;
+                for (int i = 0; i < a.n; i++) {
+                    GemvProb& p = a.p[i];
+                    p.ks_log = 0;
+                    p.xs_log = xs;
+                    p.rpad = p.ntiles * 16;
+                    p.wsp = (float*)part;
+                    part += gemv_xs_part_bytes(p.w.g.rows, a.mcount);
+                }
+            }
+        }
     }
     // phase width: whole rounds of 4 waves x U = 4 chunks, at most
     // kGemvLdsBytes of staged activations (at least one round), no wider
     // than the longest row
     const int step = kGemvWaves * gemv_u<F, M, MODE>() * F::CHUNK_COLS;
     int maxcols = 0;
-    for (int i = 0; i < a.n; i++) maxcols = maxcols > a.p[i].w.g.cols ? maxcols : a.p[i].w.g.cols;
+    for (int i = 0; i < a.n; i++) {
+        const int c = a.p[i].w.g.cols >> a.p[i].xs_log;
+        maxcols = maxcols > c ? maxcols : c;
+    }
     // bytes per column per token, x4: fp32 + sums 17, fp16 + sums 9, fp16 8
     const int per4 = MODE == kModeF32 ? 17 : MODE == kModeDot2 ? 9 : 8;
     int cap = (kGemvLdsBytes * 4 / per4 / M) / step * step;
@@ -729,7 +862,8 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
     for (int i = 0; i < a.n; i++) {
         b.p[i] = a.p[order[i]];
         b.p[i].wg_begin = wg;
-        wg += (b.p[i].ntiles + (kGemvWaves >> b.p[i].ks_log) - 1) / (kGemvWaves >> b.p[i].ks_log);
+        wg += (b.p[i].ntiles + (kGemvWaves >> b.p[i].ks_log) - 1) / (kGemvWaves >> b.p[i].ks_log)
+              << b.p[i].xs_log;
     }
     if constexpr (MODE == kModeMfma) {
         if (gsteps == 4)

@@ -70,6 +70,10 @@ _SIGS = {
     "titan_qgemm": [ctypes.POINTER(QWeightC), _P, _I, _I64, _P, _I, _I64, _I, _P],
     "titan_qgemm_batched": [ctypes.POINTER(QWeightC), ctypes.POINTER(_P), ctypes.POINTER(_P),
                             _I, _I, _I, _I, _P],
+    "titan_qgemm_workspace_bytes": [ctypes.POINTER(_I), _I, _I],
+    "titan_qgemm_ws": [ctypes.POINTER(QWeightC), _P, _I, _I64, _P, _I, _I64, _I, _P, _SZ, _P],
+    "titan_qgemm_batched_ws": [ctypes.POINTER(QWeightC), ctypes.POINTER(_P), ctypes.POINTER(_P),
+                               _I, _I, _I, _I, _P, _SZ, _P],
     "titan_qdequant": [ctypes.POINTER(QWeightC), _P, _I, _P],
     "titan_tiled_bytes": [_I, _I, _I, _I],
     "titan_repack_host": [_I, _I, _I, _I, _P, _P, _P, _P, _SZ],
@@ -115,6 +119,7 @@ def lib():
         L.titan_ckpt_close.restype = None
         L.titan_tiled_bytes.restype = _SZ
         L.titan_moe_nvfp4_workspace_bytes.restype = _SZ
+        L.titan_qgemm_workspace_bytes.restype = _SZ
         L.titan_version.restype = ctypes.c_char_p
         L.titan_status_string.restype = ctypes.c_char_p
         _LIB = L
@@ -210,29 +215,59 @@ def unpack_host(fmt, rows, cols, tiled, codes_like, scales_like=None, biases_lik
 # ---------------------------------------------------------------------------
 # compute
 # ---------------------------------------------------------------------------
-def qgemm(W, X, out_dtype=None, out=None, stream=None):
-    """Y[m] = W @ X[m] for X of shape [M, cols] (fp32/fp16/bf16 on the GPU)."""
+def qgemm_workspace_bytes(rows, M):
+    """Bytes of the K-split workspace for problems with these row counts."""
+    rows = [int(r) for r in (rows if isinstance(rows, (list, tuple)) else [rows])]
+    arr = (_I * len(rows))(*rows)
+    return int(lib().titan_qgemm_workspace_bytes(arr, len(rows), int(M)))
+
+
+def qgemm_workspace(rows, M, device="cuda"):
+    """A zero-filled workspace for qgemm(..., workspace=) / qgemm_batched."""
+    import torch
+    return torch.zeros(qgemm_workspace_bytes(rows, M), dtype=torch.uint8, device=device)
+
+
+def _ws_args(workspace):
+    return _ptr(workspace), workspace.numel() * workspace.element_size()
+
+
+def qgemm(W, X, out_dtype=None, out=None, stream=None, workspace=None):
+    """Y[m] = W @ X[m] for X of shape [M, cols] (fp32/fp16/bf16 on the GPU).
+    With `workspace` (from qgemm_workspace) small problems split K across
+    workgroups (titan_qgemm_ws)."""
     import torch
     X2 = X if X.dim() == 2 else X.view(1, -1)
     M = X2.shape[0]
     if out is None:
         out = torch.empty((M, W.rows), dtype=out_dtype or X.dtype, device=X.device)
     ws = W.cstruct()
-    _check(lib().titan_qgemm(ctypes.byref(ws), _ptr(X2), dtype_code(X2.dtype), X2.stride(0),
-                             _ptr(out), dtype_code(out.dtype), out.stride(0), M,
-                             _stream(stream)), "titan_qgemm")
+    if workspace is None:
+        _check(lib().titan_qgemm(ctypes.byref(ws), _ptr(X2), dtype_code(X2.dtype), X2.stride(0),
+                                 _ptr(out), dtype_code(out.dtype), out.stride(0), M,
+                                 _stream(stream)), "titan_qgemm")
+    else:
+        _check(lib().titan_qgemm_ws(ctypes.byref(ws), _ptr(X2), dtype_code(X2.dtype),
+                                    X2.stride(0), _ptr(out), dtype_code(out.dtype),
+                                    out.stride(0), M, *_ws_args(workspace), _stream(stream)),
+               "titan_qgemm_ws")
     return out
 
 
-def qgemm_batched(Ws, Xs, Ys, stream=None):
+def qgemm_batched(Ws, Xs, Ys, stream=None, workspace=None):
     n = len(Ws)
     arr = (QWeightC * n)(*[w.cstruct() for w in Ws])
     xs = (_P * n)(*[_ptr(x) for x in Xs])
     ys = (_P * n)(*[_ptr(y) for y in Ys])
     M = Xs[0].shape[0] if Xs[0].dim() == 2 else 1
-    _check(lib().titan_qgemm_batched(arr, xs, ys, n, dtype_code(Xs[0].dtype),
-                                     dtype_code(Ys[0].dtype), M, _stream(stream)),
-           "titan_qgemm_batched")
+    if workspace is None:
+        _check(lib().titan_qgemm_batched(arr, xs, ys, n, dtype_code(Xs[0].dtype),
+                                         dtype_code(Ys[0].dtype), M, _stream(stream)),
+               "titan_qgemm_batched")
+    else:
+        _check(lib().titan_qgemm_batched_ws(arr, xs, ys, n, dtype_code(Xs[0].dtype),
+                                            dtype_code(Ys[0].dtype), M, *_ws_args(workspace),
+                                            _stream(stream)), "titan_qgemm_batched_ws")
 
 
 class PreparedBatch:
@@ -240,19 +275,24 @@ class PreparedBatch:
     titan_qgemm_batched on the stream given at preparation (for replaying the
     same weights/activations/outputs in a decode loop)."""
 
-    def __init__(self, Ws, Xs, Ys, stream=None):
+    def __init__(self, Ws, Xs, Ys, stream=None, workspace=None):
         n = len(Ws)
-        self._keep = (Ws, Xs, Ys)
-        self._args = ((QWeightC * n)(*[w.cstruct() for w in Ws]),
-                      (_P * n)(*[_ptr(x) for x in Xs]), (_P * n)(*[_ptr(y) for y in Ys]), n,
-                      dtype_code(Xs[0].dtype), dtype_code(Ys[0].dtype),
-                      Xs[0].shape[0] if Xs[0].dim() == 2 else 1, _stream(stream))
-        self._fn = lib().titan_qgemm_batched
+        self._keep = (Ws, Xs, Ys, workspace)
+        args = ((QWeightC * n)(*[w.cstruct() for w in Ws]),
+                (_P * n)(*[_ptr(x) for x in Xs]), (_P * n)(*[_ptr(y) for y in Ys]), n,
+                dtype_code(Xs[0].dtype), dtype_code(Ys[0].dtype),
+                Xs[0].shape[0] if Xs[0].dim() == 2 else 1)
+        if workspace is None:
+            self._args = args + (_stream(stream),)
+            self._fn = lib().titan_qgemm_batched
+        else:
+            self._args = args + _ws_args(workspace) + (_stream(stream),)
+            self._fn = lib().titan_qgemm_batched_ws
 
     def __call__(self):
         st = self._fn(*self._args)
         if st:
-            _check(st, "titan_qgemm_batched")
+            _check(st, self._fn.__name__)
 
 
 def qdequant(W, out_dtype=None, stream=None):
