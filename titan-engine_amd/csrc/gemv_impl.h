@@ -553,15 +553,28 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     constexpr int DEPTH = TQ_GEMV_DEPTH;
     static_assert(DEPTH == 2 || DEPTH == 3, "load depth");
     typename F::Raw rbuf[DEPTH][U];
+    // q / gpp without a division per group: a reciprocal under-estimate
+    // (floor((2^32 - 1) / gpp)) is short by at most one for q < 2^31, and one
+    // correction step makes the quotient exact
+    const uint32_t gmag = 0xFFFFFFFFu / (uint32_t)gpp;
+    auto split_q = [&](int q, int& p, int& g) {
+        uint32_t pq = __umulhi((uint32_t)q, gmag);
+        uint32_t rq = (uint32_t)q - pq * (uint32_t)gpp;
+        if (rq >= (uint32_t)gpp) { pq++; rq -= (uint32_t)gpp; }
+        p = (int)pq;
+        g = (int)rq;
+    };
     auto load_q = [&](int q, typename F::Raw (&R)[U]) {
         const bool stream = !last_cached<F>() || q < ngroups - 1;
         q = q < ngroups ? q : ngroups - 1;
-        const int p = q / gpp;
-        load_group(p, q - p * gpp, R, stream);
+        int p, g;
+        split_q(q, p, g);
+        load_group(p, g, R, stream);
     };
     auto fold_q = [&](int q, const typename F::Raw (&R)[U]) {
-        const int p = q / gpp;
-        fold_group(p, q - p * gpp, R);
+        int p, g;
+        split_q(q, p, g);
+        fold_group(p, g, R);
     };
 #ifdef TQ_GEMV_TRACE
     const unsigned long long tr0 = __builtin_amdgcn_s_memrealtime();
