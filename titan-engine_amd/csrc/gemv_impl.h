@@ -43,6 +43,21 @@ constexpr bool last_cached() {
     else return true;
 }
 
+#ifndef TQ_GEMV_WAVES_TARGET
+#define TQ_GEMV_WAVES_TARGET 2048
+#endif
+template <class F, class = void>
+struct has_waves_target_m1 : std::false_type {};
+template <class F>
+struct has_waves_target_m1<F, std::void_t<decltype(F::WAVES_TARGET_M1)>> : std::true_type {};
+// Waves a launch aims for (the K split per row tile follows from it); a
+// format may set its own figure for one token (WAVES_TARGET_M1)
+template <class F, int M>
+constexpr long long waves_target() {
+    if constexpr (M == 1 && has_waves_target_m1<F>::value) return F::WAVES_TARGET_M1;
+    else return TQ_GEMV_WAVES_TARGET;
+}
+
 template <class F, class = void>
 struct has_sx_max_m : std::false_type {};
 template <class F>
@@ -72,9 +87,6 @@ constexpr int kGemvWaves = 4;
 constexpr int kGemvThreads = kGemvWaves * kWave;
 #ifndef TQ_GEMV_LDS_KB
 #define TQ_GEMV_LDS_KB 32
-#endif
-#ifndef TQ_GEMV_WAVES_TARGET
-#define TQ_GEMV_WAVES_TARGET 2048
 #endif
 #ifndef TQ_GEMV_DEPTH
 #define TQ_GEMV_DEPTH 2  // weight groups in flight + 1
@@ -796,7 +808,8 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
     // (target: about 2048 waves in flight, at least 8 chunks per wave)
     long long work = 0;
     for (int i = 0; i < a.n; i++) work += (long long)a.p[i].ntiles * a.p[i].nchunks;
-    const long long target = work / TQ_GEMV_WAVES_TARGET > 8 ? work / TQ_GEMV_WAVES_TARGET : 8;
+    constexpr long long wt = waves_target<F, M>();
+    const long long target = work / wt > 8 ? work / wt : 8;
     for (int i = 0; i < a.n; i++) {
         int ks = 0;
         while (ks < TQ_GEMV_KS_MAX && a.p[i].nchunks > target << ks) ks++;
