@@ -50,11 +50,17 @@ template <class F, class = void>
 struct has_waves_target_m1 : std::false_type {};
 template <class F>
 struct has_waves_target_m1<F, std::void_t<decltype(F::WAVES_TARGET_M1)>> : std::true_type {};
+template <class F, class = void>
+struct has_waves_target : std::false_type {};
+template <class F>
+struct has_waves_target<F, std::void_t<decltype(F::WAVES_TARGET)>> : std::true_type {};
 // Waves a launch aims for (the K split per row tile follows from it); a
-// format may set its own figure for one token (WAVES_TARGET_M1)
+// format may set its own figure for every token count (WAVES_TARGET) or for
+// one token (WAVES_TARGET_M1)
 template <class F, int M>
 constexpr long long waves_target() {
     if constexpr (M == 1 && has_waves_target_m1<F>::value) return F::WAVES_TARGET_M1;
+    else if constexpr (has_waves_target<F>::value) return F::WAVES_TARGET;
     else return TQ_GEMV_WAVES_TARGET;
 }
 
