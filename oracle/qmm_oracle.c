@@ -10,12 +10,22 @@
  *   or_f32_to_e4m3                         exhaustive round trip + brute-force nearest
  *   or_dequant_int4 / int2                 known-answer words; oracle/_ref (reference
  *                                          matmul_avx.cpp GEMV, bit-exact); brute force
- *   or_dequant_fp4 / nvfp4                 LUT known answers; hand-built bytes
+ *   or_dequant_fp4                         hand-built words (nibble order, group
+ *                                          of each word, per-row scale stride,
+ *                                          group sizes 8/12/16/24); exact round
+ *                                          trip of on-grid values through
+ *                                          or_quantize_fp4; error bound
+ *   or_dequant_nvfp4                       hand-built bytes (nibble order, NaN
+ *                                          scale -> 0); fp64 GEMV
  *   or_dequant_q4k / q3k                   known-answer blocks packed by an
  *                                          independent packer in tests/; every
  *                                          sub-scale position; quantize error bound
  *   or_dequant_fp8                         all 256 codes against the OCP table
  *   or_gemm_f32                            fp64 brute force
+ *   or_matvec_fmt_mt                       per format: fp64 product of the exact
+ *                                          dequantized matrix within the fp32
+ *                                          accumulation bound; one-hot columns
+ *                                          bit-exact; thread split bit-exact
  *   or_matvec_int4_cpu                     oracle/_ref (bit-exact)
  *   or_moe_topk                            hand-computed softmax / tie cases
  * No function is "parity unpinned".

@@ -388,3 +388,119 @@ def test_swiglu_and_combine():
                          np.array([4.0, 8.0], np.float32), 1.0)
     assert o.tolist() == [1.0 + 0.25 + 1.0 + 4.0, 2.0 + 0.25 - 0.5 + 8.0]
     assert np.array_equal(o, r)
+
+
+# ---------------------------------------------------------------- FP4 (fp16 group scale)
+FP4_VALUES = [0, .5, 1, 1.5, 2, 3, 4, 6, -0.0, -.5, -1, -1.5, -2, -3, -4, -6]
+
+
+def test_fp4_known_answer_words_and_groups():
+    """fp4.cu:28-84 by hand: nibble n of word p is column 8p+n, and the whole
+    word takes the scale of group (8p) // group_size of its own row."""
+    # row 0: word 0 = codes 0..7 ascending, word 1 = 15..8 descending,
+    # word 2 = 0x7 in every nibble, word 3 = 0x9 (-0.5) in every nibble;
+    # row 1: the same words rotated by one.
+    words = [0x76543210, 0x89ABCDEF, 0x77777777, 0x99999999]
+    w = np.array([words, words[1:] + words[:1]], np.uint32)
+    # group 16 -> groups {word 0, word 1} and {word 2, word 3}: scales per row
+    s = np.array([[0x3C00, 0x4000],     # 1.0, 2.0
+                  [0x3800, 0x4400]],    # 0.5, 4.0
+                 np.uint16)
+    D = O.dequant_fp4(w, s, 2, 32, 16)
+    want0 = ([FP4_VALUES[n] for n in range(8)] + [FP4_VALUES[15 - n] for n in range(8)]
+             + [12.0] * 8 + [-1.0] * 8)
+    want1 = ([0.5 * FP4_VALUES[15 - n] for n in range(8)] + [0.5 * 6.0] * 8
+             + [-2.0] * 8 + [4.0 * FP4_VALUES[n] for n in range(8)])
+    assert D[0].tolist() == want0
+    assert D[1].tolist() == want1
+    w = w[:, :3]
+    want0 = want0[:24]
+    # group 8 (one scale per word) and group 24 (all three words share one)
+    s8 = np.array([[0x3C00, 0x4000, 0x3400]] * 2, np.uint16)   # 1, 2, 0.25
+    D8 = O.dequant_fp4(w[:1], s8[:1], 1, 24, 8)[0]
+    assert D8[:8].tolist() == want0[:8]
+    assert D8[8:16].tolist() == [2.0 * FP4_VALUES[15 - n] for n in range(8)]
+    assert D8[16:].tolist() == [1.5] * 8
+    D24 = O.dequant_fp4(w[:1], np.array([[0x4000]], np.uint16), 1, 24, 24)[0]
+    assert D24.tolist() == [2.0 * v for v in want0[:16]] + [12.0] * 8
+    # a group size that is not a multiple of 8: word p uses group (8p) // 12,
+    # so word 1 (columns 8..15) still takes group 0's scale
+    s12 = np.array([[0x3C00, 0x4000]], np.uint16)
+    D12 = O.dequant_fp4(w[:1], s12, 1, 24, 12)[0]
+    assert D12[:16].tolist() == want0[:16]
+    assert D12[16:].tolist() == [12.0] * 8
+    # signed zero of code 8 survives the scale
+    assert struct.pack("<f", float(D[0][8 + 7])) == struct.pack("<f", -0.0)
+
+
+def test_fp4_quantize_dequantize_round_trip(rng):
+    """Values on the E2M1 grid times a power-of-two group scale come back
+    exactly through or_quantize_fp4 -> or_dequant_fp4 (scale = amax/6 is then
+    exact in fp16); random values come back within one grid step."""
+    rows, cols, gs = 8, 256, 32
+    q = rng.integers(0, 16, (rows, cols))
+    q[:, ::gs] = 7                                  # every group holds +6 -> amax = 6s
+    scale = 2.0 ** rng.integers(-12, 3, (rows, cols // gs))
+    W = (np.array(FP4_VALUES, np.float64)[q] * np.repeat(scale, gs, 1)).astype(np.float32)
+    w, s = O.quantize_fp4(W, gs)
+    D = O.dequant_fp4(w, s, rows, cols, gs)
+    assert np.array_equal(D, W)
+    Wr = rng.normal(0, 0.02, (rows, cols)).astype(np.float32)
+    w, s = O.quantize_fp4(Wr, gs)
+    D = O.dequant_fp4(w, s, rows, cols, gs)
+    sc = O.f16_bits_to_f32(s).astype(np.float64)
+    amax = np.abs(Wr.reshape(rows, -1, gs)).max(-1)
+    # the widest E2M1 gap is 2 (4 -> 6): half of it in units of the scale, plus
+    # the fp16 rounding of the scale times the largest code
+    bound = sc * 1.0 + 6 * np.abs(sc - amax / 6) + 1e-9
+    err = np.abs(D - Wr).reshape(rows, -1, gs).max(-1)
+    assert np.all(err <= bound)
+
+
+# ---------------------------------------------------------------- per-format row GEMV
+def _fmt_operands(fmt, rng, rows, cols):
+    W = rng.normal(0, 0.02, (rows, cols)).astype(np.float32)
+    z16 = np.zeros(1, np.uint16)
+    if fmt == "int4":
+        w, s, b = O.quantize_int4(W, 128)
+        return (w, s, b, 1.0, 128), O.dequant_int4(w, s, b, rows, cols, 128)
+    if fmt == "int2":
+        w, s, b = O.quantize_int2(W, 64)
+        return (w, s, b, 1.0, 64), O.dequant_int2(w, s, b, rows, cols, 64)
+    if fmt == "nvfp4":
+        g = float(np.abs(W).max() / (6 * 448))
+        w, s = O.quantize_nvfp4(W, g)
+        return (w, s, z16, g, 16), O.dequant_nvfp4(w, s, g, rows, cols)
+    if fmt == "q4k":
+        blk = O.quantize_q4k(W)
+        return (blk, z16, z16, 1.0, 256), O.dequant_q4k(blk, rows, cols)
+    if fmt == "q3k":
+        blk = O.quantize_q3k(W)
+        return (blk, z16, z16, 1.0, 256), O.dequant_q3k(blk, rows, cols)
+    w, cs = O.quantize_fp8_rows(W)
+    return (w, cs, z16, 1.0, 1), O.dequant_fp8(w, cs, rows, cols)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int2", "nvfp4", "q4k", "q3k", "fp8"])
+def test_matvec_fmt_mt_matches_fp64(fmt, rng):
+    """or_matvec_fmt_mt (the reference for the full-size GPU GEMV tests) is
+    the fp64 product of the exact dequantized matrix up to fp32 accumulation
+    error; every row reads its own codes and scales (rows differ, so a wrong
+    row stride fails), and the thread split does not change a bit."""
+    rows, cols = 37, 1536
+    (codes, s, b, g, gs), D = _fmt_operands(fmt, rng, rows, cols)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    y1 = O.matvec_fmt_mt(fmt, codes, s, b, g, gs, x, rows, cols, 1)
+    ref = O.gemm_f64(D, x)[0]
+    # fp32 accumulation of `cols` terms: |err| <= cols * 2^-24 * sum |w x|
+    bound = cols * 2.0 ** -24 * (np.abs(D.astype(np.float64)) @ np.abs(x.astype(np.float64)))
+    assert np.all(np.abs(y1 - ref) <= bound)
+    assert np.abs(y1 - ref).max() <= 1e-5 * np.abs(ref).max()
+    y5 = O.matvec_fmt_mt(fmt, codes, s, b, g, gs, x, rows, cols, 5)
+    assert np.array_equal(y1.view(np.uint32), y5.view(np.uint32))
+    # one-hot x returns one dequantized column exactly (fma(w, 1, 0) = w)
+    for c in (0, 255, 256, cols - 1):
+        e = np.zeros(cols, np.float32)
+        e[c] = 1.0
+        col = O.matvec_fmt_mt(fmt, codes, s, b, g, gs, e, rows, cols, 3)
+        assert np.array_equal(col, D[:, c]), (fmt, c)
