@@ -140,9 +140,12 @@ int titan_qgemm_batched(const titan_qweight* Ws, const void* const* Xs, void* co
  * titan_qgemm_batched.
  * `workspace` is a caller-owned device buffer of at least
  * titan_qgemm_workspace_bytes() bytes, 256-byte aligned, zero-filled once
- * before its first use; every call leaves its counters at zero again, so it
- * can be reused by later calls ordered after it on a stream.  Calls that
- * share one workspace must not overlap.  Results are deterministic (the
+ * before its first use; every call leaves its counters at zero again, and the
+ * counters of every call sit in one fixed region at the start of the
+ * workspace that no partial sum overlaps, so a workspace can be reused by any
+ * later call (other problem sets, other token counts) ordered after it on a
+ * stream, provided it is large enough for that call.  Calls that share one
+ * workspace must not overlap.  Results are deterministic (the
  * partial sums are added in a fixed order). */
 size_t titan_qgemm_workspace_bytes(const int* rows, int n, int M);
 int titan_qgemm_ws(const titan_qweight* W, const void* X, int x_dtype, int64_t ldx,

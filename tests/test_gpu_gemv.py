@@ -321,3 +321,27 @@ def test_kquant_int2_full_size(fmt, n, k, M):
     for t in sorted({0, M - 1}):
         ref = O.matvec_fmt_mt(fmt, codes, s16, b16, 1.0, gs, x[t].float().cpu().numpy(), n, k, 8)
         assert_close_out(to_np(y[t]), ref.astype(np.float64), "f32")
+
+
+@pytest.mark.parametrize("fmt", ["q4k", "q3k"])
+@pytest.mark.parametrize("M", [1, 4])
+def test_kquant_llama8b_layer_full_size(fmt, M):
+    """The Llama-3-8B layer in Q4_K / Q3_K (bench's synthetic K-quant layer,
+    one batched launch): the 14336-column rows run with the per-format K split
+    the launch heuristics pick at this shape; every output of the first and
+    last token against the oracle's fp32 GEMV of the same ggml bytes."""
+    import bench
+    f = tq.Q4_K if fmt == "q4k" else tq.Q3_K
+    gen = torch.Generator(device="cuda").manual_seed(21 + M + f)
+    blks = [bench.random_kquant(f, n, k, gen) for _, n, k in bench.LLAMA8B]
+    Ws = [tq.QWeight(f, tq.LAYOUT_TILED, n, k, torch.from_numpy(tq.repack_host(f, n, k, b)).cuda())
+          for (_, n, k), b in zip(bench.LLAMA8B, blks)]
+    X = {k: torch.randn(M, k, generator=gen, device="cuda").half() for k in (4096, 14336)}
+    Xs = [X[k] for _, _, k in bench.LLAMA8B]
+    Ys = [torch.empty(M, n, device="cuda", dtype=torch.float32) for _, n, _ in bench.LLAMA8B]
+    tq.qgemm_batched(Ws, Xs, Ys)
+    torch.cuda.synchronize()
+    for (_, n, k), b, y in zip(bench.LLAMA8B, blks, Ys):
+        for t in sorted({0, M - 1}):
+            ref = O.matvec_fmt_mt(fmt, b, None, None, 1.0, 0, X[k][t].float().cpu().numpy(), n, k, 8)
+            assert_close_out(to_np(y[t]), ref.astype(np.float64), "f32")

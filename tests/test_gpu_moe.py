@@ -185,15 +185,17 @@ def test_moe_nvfp4_every_scale_byte(rng):
     assert_close_out(out.cpu().numpy().astype(np.float64), want, "f32")
 
 
-def test_moe_nvfp4_deepseek_size():
+@pytest.mark.parametrize("T", [64, 1024])
+def test_moe_nvfp4_deepseek_size(T):
     """The benchmark layer at its real size (256 experts, top-8, hidden 7168,
-    inter 2048, T = 64 with GPU routing): three sampled tokens against the
+    inter 2048, T = 64 decode and T = 1024 prefill tokens with GPU routing;
+    T = 1024 runs the 48/64-token passes per expert): sampled tokens against the
     reference's expert loop restated by the oracle (fp4.cu:187-252 GEMVs with
     the activations rounded to fp16 as they enter the matrix cores, SwiGLU,
     the fp16 activation the kernel stores, weighted sum in slot order)."""
     import bench
-    gen = torch.Generator(device="cuda").manual_seed(5)
-    E, hidden, inter, k, T = 256, 7168, 2048, 8, 64
+    gen = torch.Generator(device="cuda").manual_seed(5 + T)
+    E, hidden, inter, k = 256, 7168, 2048, 8
     mats, table = bench.make_nvfp4_experts(E, hidden, inter, gen)
     logits = torch.randn(T, E, generator=gen, device="cuda")
     x = torch.randn(T, hidden, generator=gen, device="cuda").to(torch.bfloat16)
@@ -217,7 +219,13 @@ def test_moe_nvfp4_deepseek_size():
             parts[(e, j)] = (c, s)
         return parts[(e, j)]
 
-    for t in (0, 31, 63):
+    # T = 1024: all 256 experts hold tokens; check the first, last and two
+    # middle tokens plus the token routed to the most loaded expert
+    toks = {0, T // 2 - 1, T - 1}
+    if T > 64:
+        load = np.bincount(idx.ravel(), minlength=E)
+        toks |= {T // 3, int(np.flatnonzero((idx == load.argmax()).any(1))[-1])}
+    for t in sorted(toks):
         acc = np.zeros(hidden, np.float64)
         for q in range(k):
             e = int(idx[t, q])

@@ -67,6 +67,40 @@ def test_splitk_config_shapes(fmt, rows, cols, gs, M, rng):
     assert_close_out(to_np(base), ref, "f16")
 
 
+@pytest.mark.parametrize("fmt,n,k", [("q3k", 28672, 8192), ("int2", 28672, 8192),
+                                     ("q3k", 8192, 8192), ("int2", 8192, 28672)])
+@pytest.mark.parametrize("M", [1, 4])
+def test_workspace_full_size_70b(fmt, n, k, M):
+    """The large 70B shapes with a caller workspace, as a caller passes it:
+    whichever split the launch heuristics pick, every output row of the first
+    and last token matches the oracle's fp32 GEMV of the same REF bytes, and
+    the results equal the launch without a workspace within the same bar."""
+    import bench
+    from oracle import oracle_ctypes as O
+    gen = torch.Generator(device="cuda").manual_seed(3 * n + k + M)
+    if fmt == "int2":
+        (m,) = bench.make_int4_layer(gen, gs=64, bits=2, shapes=[("w", n, k)])
+        W = tq.QWeight(tq.INT2, tq.LAYOUT_TILED, n, k, m["tiled"], group_size=64)
+        w, s, b = (t.cpu().numpy() for t in m["ref"])
+        codes, s16, b16, gs = w.view(np.uint32), s.view(np.uint16), b.view(np.uint16), 64
+    else:
+        blk = bench.random_kquant(tq.Q3_K, n, k, gen)
+        W = tq.QWeight(tq.Q3_K, tq.LAYOUT_TILED, n, k,
+                       torch.from_numpy(tq.repack_host(tq.Q3_K, n, k, blk)).cuda())
+        codes, s16, b16, gs = blk, None, None, 0
+    x = torch.randn(M, k, generator=gen, device="cuda").half()
+    ws = tq.qgemm_workspace(n, M)
+    y = tq.qgemm(W, x, out_dtype=torch.float32, workspace=ws)
+    y2 = tq.qgemm(W, x, out_dtype=torch.float32, workspace=ws)
+    base = tq.qgemm(W, x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    for t in sorted({0, M - 1}):
+        ref = O.matvec_fmt_mt(fmt, codes, s16, b16, 1.0, gs, x[t].float().cpu().numpy(), n, k, 8)
+        assert_close_out(to_np(y[t]), ref.astype(np.float64), "f32")
+        assert_close_out(to_np(base[t]), ref.astype(np.float64), "f32")
+
+
 def test_splitk_workspace_reuse_across_shapes(rng):
     """One workspace serves a large call, a smaller call and the large call
     again: the counters left by each call must be zero for the next."""
@@ -88,6 +122,27 @@ def test_splitk_workspace_reuse_across_shapes(rng):
     yf = tq.qgemm(Wb, xf, out_dtype=torch.float32, workspace=tq.qgemm_workspace(256, 11))
     torch.cuda.synchronize()
     assert_close_out(to_np(yf), xf64 @ big["deq"].astype(np.float64).T, "f32")
+
+
+def test_splitk_workspace_reuse_across_problem_sets(rng):
+    """One workspace serves a one-problem call, then a two-problem batched
+    call: the second problem's counters must not land on the partial sums the
+    first call left (they sit in their own region), so both calls match the
+    oracle and a repeat of each gives the same bits."""
+    ds = [make_weights("int2", 1024, 8192, rng, gs=64) for _ in range(2)]
+    Ws = [upload(d, tq.LAYOUT_TILED) for d in ds]
+    ws = tq.qgemm_workspace([1024, 1024], 4)
+    for M in (1, 4):
+        X = [act(M, 8192, "f16", rng) for _ in range(2)]
+        y1 = tq.qgemm(Ws[0], X[0][0], out_dtype=torch.float32, workspace=ws)
+        Ys = [torch.zeros(M, 1024, dtype=torch.float32, device="cuda") for _ in range(2)]
+        tq.qgemm_batched(Ws, [x for x, _ in X], Ys, workspace=ws)
+        y1b = tq.qgemm(Ws[0], X[0][0], out_dtype=torch.float32, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y1b)
+        assert_close_out(to_np(y1), X[0][1] @ ds[0]["deq"].astype(np.float64).T, "f32")
+        for d, (_, x64), Y in zip(ds, X, Ys):
+            assert_close_out(to_np(Y), x64 @ d["deq"].astype(np.float64).T, "f32")
 
 
 @pytest.mark.parametrize("lay", list(LAYOUTS))

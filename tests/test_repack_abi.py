@@ -203,11 +203,13 @@ def test_every_entry_point_rejects_bad_arguments():
     assert L.titan_gemv_fp32(p, p, p, 16, -1, N) == E
     assert L.titan_fp8_quantize_rows(p, tq.BF16, 0, 128, p, p, N) == E
     assert L.titan_swiglu(p, p, p, 0, N) == E
-    # K-split workspace: one counter region per problem, 16 parts of partials
+    # K-split workspace: one fixed 8 KiB counter region (2048 tile groups),
+    # then 16 parts of fp32 partials per token (at most 32 tokens a launch)
+    # for every problem, rows rounded up to whole 16-row tiles
     rows = (ctypes.c_int * 2)(4096, 1000)
     one = L.titan_qgemm_workspace_bytes(rows, 1, 1)
-    assert one == 16 * 4096 * 4 + 1024
-    assert L.titan_qgemm_workspace_bytes(rows, 2, 1) == one + (16 * 1008 * 4 + 252 + 255) // 256 * 256
-    assert L.titan_qgemm_workspace_bytes(rows, 1, 64) == 32 * one - 31 * 1024
+    assert one == 8192 + 16 * 4096 * 4
+    assert L.titan_qgemm_workspace_bytes(rows, 2, 1) == one + 16 * 1008 * 4
+    assert L.titan_qgemm_workspace_bytes(rows, 1, 64) == 8192 + 32 * 16 * 4096 * 4
     assert L.titan_qgemm_workspace_bytes(rows, 0, 1) == 0
     assert L.titan_qgemm_workspace_bytes(N, 1, 1) == 0

@@ -225,10 +225,10 @@ extern "C" int titan_qgemm_batched(const titan_qweight* Ws, const void* const* X
 extern "C" size_t titan_qgemm_workspace_bytes(const int* rows, int n, int M) {
     if (!rows || n <= 0 || n > TITAN_MAX_BATCH || M <= 0) return 0;
     const int m = M < 32 ? M : 32;  // tokens per launch at most
-    size_t b = 0;
+    size_t b = kGemvXsCntBytes;
     for (int i = 0; i < n; i++) {
         if (rows[i] <= 0) return 0;
-        b += gemv_xs_bytes(rows[i], m);
+        b += gemv_xs_part_bytes(rows[i], m);
     }
     return b;
 }

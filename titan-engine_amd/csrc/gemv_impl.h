@@ -144,15 +144,18 @@ struct GemvArgs {
 #define TQ_GEMV_XS_MAX_LOG 4   // at most 16 workgroups share a row tile
 #endif
 
-// Workspace of the cross-workgroup K split.  Every problem's counters (one
-// int per row tile, 256-byte rounded) come first, at offsets that do not
-// depend on the token count, so that launches with different token counts
-// can share one workspace; the partials [16][m][rpad] fp32 follow.
-inline size_t gemv_xs_cnt_bytes(int rows) { return ((size_t)(rows + 15) / 16 * 4 + 255) / 256 * 256; }
+// Workspace of the cross-workgroup K split.  The counters (one int per tile
+// group) of every problem of a call live in one fixed region at the start of
+// the workspace, indexed by the call's running tile count: the split engages
+// only below TQ_GEMV_XS_WAVES row tiles in total, so every counter of every
+// call falls in that region, which nothing else writes.  Calls with other
+// problem sets and token counts can therefore share one workspace: the
+// counters a call finds are the zeros the previous call left.  The partials
+// [16][m][rpad] fp32 of each problem follow the counter region.
+constexpr size_t kGemvXsCntBytes = (size_t)TQ_GEMV_XS_WAVES * 4;
 inline size_t gemv_xs_part_bytes(int rows, int m) {
     return (size_t)m * ((size_t)(rows + 15) / 16 * 16) * 4 << TQ_GEMV_XS_MAX_LOG;
 }
-inline size_t gemv_xs_bytes(int rows, int m) { return gemv_xs_cnt_bytes(rows) + gemv_xs_part_bytes(rows, m); }
 
 // fp32 activations in column order plus fp32 sums of every 16 columns.
 template <int M>
@@ -341,7 +344,20 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     // Each of the KS waves takes a contiguous quarter (half) of the phase, so
     // a group is U consecutive chunks starting at a multiple of U.
     const int pspan = pchunks >> ks_log;
+#ifndef TQ_GEMV_ROT
+#define TQ_GEMV_ROT 0
+#endif
+#if TQ_GEMV_ROT
+    // waves start their walk over a phase's groups at different groups
+    const int rot = (int)(((unsigned)tile * (unsigned)TQ_GEMV_ROT + (unsigned)pi * 5u + (unsigned)xpart * 3u) % (unsigned)gpp);
+    auto chunk_at = [&](int ph, int g, int u) {
+        int gg = g + rot;
+        gg = gg >= gpp ? gg - gpp : gg;
+        return ph * pchunks + part * pspan + gg * U + u;
+    };
+#else
     auto chunk_at = [&](int ph, int g, int u) { return ph * pchunks + part * pspan + g * U + u; };
+#endif
     // stream: nontemporal code loads.  For LAST_CACHED formats the wave's
     // last group is loaded cached, so that the repeated loads past it (below)
     // hit the cache instead of fetching the group from memory again.
@@ -810,8 +826,9 @@ template <class F, int M, int MODE>
 void launch_mode(GemvArgs& a, int, hipStream_t st) {
     const int gsteps = a.p[0].gsteps;  // MFMA: word steps per scale group (same for all problems)
     // K split per problem so that every wave folds a similar number of
-    // chunks (long rows are shared by 2 or 4 waves)
-    // (target: about 2048 waves in flight, at least 8 chunks per wave)
+    // chunks (long rows are shared by 2 or 4 waves); the wave count aimed for
+    // is waves_target<F, M>() (TQ_GEMV_WAVES_TARGET unless the format sets
+    // its own), with at least 8 chunks per wave
     long long work = 0;
     for (int i = 0; i < a.n; i++) work += (long long)a.p[i].ntiles * a.p[i].nchunks;
     constexpr long long wt = waves_target<F, M>();
@@ -830,11 +847,16 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
     // 13.8 -> 11.7 us; for the 128-column-chunk formats (INT4, Q4_K 4096^2:
     // 8.2 -> 10.2 us) the partials' round trips cost more than the extra
     // waves gain, so they keep the single-workgroup tiles.
+    // The split aims for the same wave count as the in-workgroup split (the
+    // smaller of TQ_GEMV_XS_WAVES and the format's target): a launch that the
+    // format's target already considers full (Q3_K / INT2 28672 x 8192 at
+    // 1792 waves against a 1536 target) keeps its single-workgroup tiles.
     if (a.ws && F::CHUNK_COLS > 128) {
         constexpr int U = gemv_u<F, M, MODE>();
+        constexpr long long xs_waves = wt < TQ_GEMV_XS_WAVES ? wt : TQ_GEMV_XS_WAVES;
         long long waves = 0;
         for (int i = 0; i < a.n; i++) waves += (long long)a.p[i].ntiles << a.p[i].ks_log;
-        if (waves < TQ_GEMV_XS_WAVES) {
+        if (waves < xs_waves) {
             int xs = 0;
             long long w0 = 0;
             for (int i = 0; i < a.n; i++) w0 += a.p[i].ntiles;
@@ -843,16 +865,18 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
                     if ((a.p[i].nchunks >> x) < U || (a.p[i].nchunks % (U << x)) != 0) return false;
                 return true;
             };
-            while (xs < TQ_GEMV_XS_MAX_LOG && (w0 << xs) < TQ_GEMV_XS_WAVES && fits(xs + 1)) xs++;
-            size_t need = 0;
-            for (int i = 0; i < a.n; i++) need += gemv_xs_bytes(a.p[i].w.g.rows, a.mcount);
+            while (xs < TQ_GEMV_XS_MAX_LOG && (w0 << xs) < xs_waves && fits(xs + 1)) xs++;
+            static_assert(xs_waves <= TQ_GEMV_XS_WAVES, "counter region holds TQ_GEMV_XS_WAVES tiles");
+            size_t need = kGemvXsCntBytes;
+            for (int i = 0; i < a.n; i++) need += gemv_xs_part_bytes(a.p[i].w.g.rows, a.mcount);
+            // w0 << xs < xs_waves: fewer tiles than the counter region holds
             if (xs > 0 && (w0 << xs) > waves && need <= a.ws_bytes) {
-                char* cnt = (char*)a.ws;
+                int tiles = 0;
                 for (int i = 0; i < a.n; i++) {
-                    a.p[i].wsc = (int*)cnt;
-                    cnt += gemv_xs_cnt_bytes(a.p[i].w.g.rows);
+                    a.p[i].wsc = (int*)a.ws + tiles;
+                    tiles += a.p[i].ntiles;
                 }
-                char* part = cnt;
+                char* part = (char*)a.ws + kGemvXsCntBytes;
                 for (int i = 0; i < a.n; i++) {
                     GemvProb& p = a.p[i];
                     p.ks_log = 0;
