@@ -44,7 +44,8 @@ enum {
     TITAN_ERR_LAUNCH = -3,        /* hipGetLastError() after the launch */
     TITAN_ERR_WORKSPACE = -4,     /* workspace missing or too small */
     TITAN_ERR_IO = -5,            /* checkpoint file missing, unreadable or malformed */
-    TITAN_ERR_NOT_FOUND = -6      /* no such tensor in the checkpoint */
+    TITAN_ERR_NOT_FOUND = -6,     /* no such tensor in the checkpoint */
+    TITAN_ERR_SCRATCH_LIMIT = -7  /* needs more than the static scratch (TITAN_NOALLOC_SCRATCH_BYTES) */
 };
 
 /* ---- element / weight formats --------------------------------------------
@@ -154,6 +155,22 @@ int titan_qgemm_ws(const titan_qweight* W, const void* X, int x_dtype, int64_t l
 int titan_qgemm_batched_ws(const titan_qweight* Ws, const void* const* Xs, void* const* Ys,
                            int n, int x_dtype, int y_dtype, int M, void* workspace,
                            size_t workspace_bytes, hipStream_t stream);
+
+/* titan_qgemm_batched_ws with the workspace in a static device array that the
+ * library holds on every GPU it runs on until the process ends, so the call
+ * allocates nothing (no hipMalloc, no library allocation).  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Returns TITAN_ERR_SCRATCH_LIMIT, before any device work, when
+ * titan_qgemm_workspace_bytes(rows, n, M) exceeds TITAN_NOALLOC_SCRATCH_BYTES
+ * (32 MiB: e.g. 4096 rows at 32 tokens, or 28672 rows at 16 tokens).  Every
+ * call on one GPU shares that GPU's array (the first call on a device clears
+ * its counters with a kernel on `stream`; every call leaves them at zero):
+ * calls on one GPU must be ordered (one stream, or synchronised); calls that
+ * overlap on one GPU race.  Results equal titan_qgemm_batched_ws bit for bit. */
+#define TITAN_NOALLOC_SCRATCH_BYTES (32u << 20)
+int titan_qgemm_batched_noalloc(const titan_qweight* Ws, const void* const* Xs, void* const* Ys,
+                                int n, int x_dtype, int y_dtype, int M, hipStream_t stream);
 
 /* Exact dequantization: out[r][c] (out_dtype FP32 is bit-exact with the
  * reference's dequantized value; FP16/BF16 round it to nearest-even). */

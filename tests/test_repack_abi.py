@@ -178,6 +178,7 @@ def test_every_entry_point_rejects_bad_arguments():
         "titan_qgemm_ws": (N, N, tq.FP16, 128, N, tq.FP16, 16, 1, N, ctypes.c_size_t(0), N),
         "titan_qgemm_batched_ws": (ctypes.byref(W), N, N, 0, tq.FP16, tq.FP16, 1, N,
                                    ctypes.c_size_t(0), N),
+        "titan_qgemm_batched_noalloc": (ctypes.byref(W), N, N, 0, tq.FP16, tq.FP16, 1, N),
         "titan_qdequant": (N, N, tq.FP32, N),
         "titan_fp8_quantize_rows": (N, tq.BF16, 1, 128, N, N, N),
         "titan_fp8_gemm": (N, N, N, N, N, tq.BF16, 128, 128, 128, N),
@@ -213,3 +214,23 @@ def test_every_entry_point_rejects_bad_arguments():
     assert L.titan_qgemm_workspace_bytes(rows, 1, 64) == 8192 + 32 * 16 * 4096 * 4
     assert L.titan_qgemm_workspace_bytes(rows, 0, 1) == 0
     assert L.titan_qgemm_workspace_bytes(N, 1, 1) == 0
+
+
+def test_noalloc_rejects_beyond_static_scratch():
+    """titan_qgemm_batched_noalloc refuses, before any device work (so this
+    runs without a GPU), a call whose K-split workspace would exceed the
+    library's static scratch, with its own status."""
+    import ctypes
+    L = tq.lib()
+    rows = (ctypes.c_int * 8)(*([4096] * 8))
+    assert L.titan_qgemm_workspace_bytes(rows, 8, 32) > tq.NOALLOC_SCRATCH_BYTES
+    assert L.titan_qgemm_workspace_bytes(rows, 1, 32) <= tq.NOALLOC_SCRATCH_BYTES
+    Ws = (tq.QWeightC * 8)()
+    for w in Ws:
+        w.format, w.layout, w.rows, w.cols, w.group_size = tq.INT4, tq.LAYOUT_TILED, 4096, 1024, 128
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    xs = (ctypes.c_void_p * 8)(*([p] * 8))
+    assert L.titan_qgemm_batched_noalloc(Ws, xs, xs, 8, tq.FP16, tq.FP16, 32, None) == tq.ERR_SCRATCH_LIMIT
+    assert L.titan_status_string(tq.ERR_SCRATCH_LIMIT).startswith(b"problem needs more than the static scratch")
+    assert L.titan_qgemm_batched_noalloc(Ws, xs, xs, 8, tq.FP16, tq.FP16, 0, None) == tq.ERR_INVALID_ARG

@@ -368,6 +368,7 @@ extern "C" const char* titan_status_string(int s) {
         case TITAN_ERR_WORKSPACE: return "workspace missing or too small";
         case TITAN_ERR_IO: return "checkpoint file missing, unreadable or malformed";
         case TITAN_ERR_NOT_FOUND: return "tensor not found";
+        case TITAN_ERR_SCRATCH_LIMIT: return "problem needs more than the static scratch (TITAN_NOALLOC_SCRATCH_BYTES)";
         default: return "unknown status";
     }
 }

@@ -16,6 +16,8 @@ LIB_PATH = os.path.join(HERE, "libtitan_qmm.so")
 
 # status / enums (include/titan_qmm.h)
 OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_WORKSPACE = 0, -1, -2, -3, -4
+ERR_SCRATCH_LIMIT = -7
+NOALLOC_SCRATCH_BYTES = 32 << 20
 ERR_IO, ERR_NOT_FOUND = -5, -6
 FP32, FP16, BF16 = 0, 1, 2
 FP8_E4M3, FP4, INT4, INT2, Q4_K, Q3_K, NVFP4 = 3, 5, 7, 8, 9, 10, 32
@@ -72,6 +74,8 @@ _SIGS = {
                             _I, _I, _I, _I, _P],
     "titan_qgemm_workspace_bytes": [ctypes.POINTER(_I), _I, _I],
     "titan_qgemm_ws": [ctypes.POINTER(QWeightC), _P, _I, _I64, _P, _I, _I64, _I, _P, _SZ, _P],
+    "titan_qgemm_batched_noalloc": [ctypes.POINTER(QWeightC), ctypes.POINTER(_P), ctypes.POINTER(_P),
+                                    _I, _I, _I, _I, _P],
     "titan_qgemm_batched_ws": [ctypes.POINTER(QWeightC), ctypes.POINTER(_P), ctypes.POINTER(_P),
                                _I, _I, _I, _I, _P, _SZ, _P],
     "titan_qdequant": [ctypes.POINTER(QWeightC), _P, _I, _P],
@@ -268,6 +272,19 @@ def qgemm_batched(Ws, Xs, Ys, stream=None, workspace=None):
         _check(lib().titan_qgemm_batched_ws(arr, xs, ys, n, dtype_code(Xs[0].dtype),
                                             dtype_code(Ys[0].dtype), M, *_ws_args(workspace),
                                             _stream(stream)), "titan_qgemm_batched_ws")
+
+
+def qgemm_batched_noalloc(Ws, Xs, Ys, stream=None):
+    """qgemm_batched with the K-split workspace in the library's static device
+    scratch (titan_qgemm_batched_noalloc): allocates nothing."""
+    n = len(Ws)
+    arr = (QWeightC * n)(*[w.cstruct() for w in Ws])
+    xs = (_P * n)(*[_ptr(x) for x in Xs])
+    ys = (_P * n)(*[_ptr(y) for y in Ys])
+    M = Xs[0].shape[0] if Xs[0].dim() == 2 else 1
+    _check(lib().titan_qgemm_batched_noalloc(arr, xs, ys, n, dtype_code(Xs[0].dtype),
+                                             dtype_code(Ys[0].dtype), M, _stream(stream)),
+           "titan_qgemm_batched_noalloc")
 
 
 class PreparedBatch:
