@@ -50,6 +50,35 @@ TQ_DEV f4_t mfma16(h4_t a, h4_t b, f4_t c) { return __builtin_amdgcn_mfma_f32_16
 TQ_DEV f4_t mfma32(h8_t a, h8_t b, f4_t c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 TQ_DEV f4_t f4_zero() { return (f4_t){0.f, 0.f, 0.f, 0.f}; }
 
+// Code-plane source of one wave (tiled layouts): the 1 KiB chunks of the
+// wave's row tile that its workgroup folds (base, bytes) and the lane's
+// 16-byte offset inside a chunk.  at(c) is a buffer resource starting at
+// chunk c; reads at or past the end of the range return zeros without a
+// memory access (the hardware's range check), so the loads a wave issues
+// past its last group cost no bandwidth.
+struct CodeSrc {
+    const uint8_t* base;
+    uint32_t bytes;
+    uint32_t lane;
+    TQ_DEV __amdgpu_buffer_rsrc_t at(int c) const {
+        const uint32_t o = (uint32_t)c * 1024u;
+        // signed max (a scalar instruction; an unsigned saturating subtraction
+        // would be a vector one and make the resource a per-lane value);
+        // a tile's chunk range is far below 2^31 bytes
+        const int d = (int)bytes - (int)o;
+        const uint32_t n = (uint32_t)(d > 0 ? d : 0);
+        // 0x00020000: raw buffer, 32-bit data format (word 3 of the descriptor)
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(base + o), (short)0, (int)n, 0x00020000);
+    }
+};
+// Chunk u of a group whose first chunk `rs` starts at (nontemporal: cache
+// policy 2); the chunk offset is an immediate of the instruction.
+template <bool NT>
+TQ_DEV uint4 ld_code_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t lane, int u) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane + (uint32_t)u * 1024u, 0,
+                                                                           NT ? 2 : 0));
+}
+
 // E2M1 codes of a word as fp16 pairs (value = lut * 2^-14): nibbles n and
 // n + 4 of word w become the low / high halves of fp4_pair(w, n).
 TQ_DEV uint32_t fp4_pair(uint32_t w, int n) {
@@ -133,12 +162,13 @@ struct FxNib {
             return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_sb_off(g, row, 0), 0u};
     }
     template <int GS, bool NT = true>
-    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
+    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r, __amdgpu_buffer_rsrc_t rs,
+                            uint32_t lane, int u) {
         if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
 #pragma unroll
             for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
         } else {
-            uint4 q = ld_codes_u128<NT>(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_code_chunk<NT>(rs, lane, u);
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
         if constexpr (SB_CELL) return;  // load_cell
@@ -177,7 +207,7 @@ struct FxNib {
     // multiples of 4).
     template <int GS>
     TQ_DEV static void load_cell(const WDesc& w, const Off& o, int c, Raw& r) {
-        r.q = ld_u128(w.codes + (o.s + (uint32_t)(c / GS) * 256u));
+        r.q = ld_u128((w.codes + (size_t)(((uint32_t)c / GS) * 256u)) + o.s);
     }
     template <int GS>
     TQ_DEV static Dec decode_cell(const uint4& q, int u) {
@@ -326,7 +356,7 @@ template <int L> using FxFp4 = FxNib<L, true>;
 template <int LAYOUT>
 struct FxInt2 {
     static constexpr int FMT = TITAN_INT2, CHUNK_COLS = 256;
-    static constexpr bool HAS_MFMA = true, PIPE = true, LAST_CACHED = false;
+    static constexpr bool HAS_MFMA = true, PIPE = true;
     // several tokens: fewer, longer waves than the default 2048 measured 22%
     // faster on 28672x8192 at four tokens (42.6 -> 33.2 us), the other shapes
     // unchanged; one token keeps 2048 (28672x8192 1.5% slower with 1536)
@@ -344,12 +374,13 @@ struct FxInt2 {
             return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_sb_off(g, row, 0), 0u};
     }
     template <int GS, bool NT = true>
-    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
+    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r, __amdgpu_buffer_rsrc_t rs,
+                            uint32_t lane, int u) {
         if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
 #pragma unroll
             for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
         } else {
-            uint4 q = ld_codes_u128<NT>(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_code_chunk<NT>(rs, lane, u);
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
         if constexpr (SB_CELL) return;  // load_cell
@@ -386,7 +417,7 @@ struct FxInt2 {
     // multiples of 4).
     template <int GS>
     TQ_DEV static void load_cell(const WDesc& w, const Off& o, int c, Raw& r) {
-        r.q = ld_u128(w.codes + (o.s + (uint32_t)(c / GS) * 256u));
+        r.q = ld_u128(w.codes + (o.s + ((uint32_t)c / GS) * 256u));
     }
     template <int GS>
     TQ_DEV static Dec decode_cell(const uint4& q, int u) {
@@ -545,7 +576,8 @@ struct FxNvfp4 {
             return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_nvs_off(g, row, 0)};
     }
     template <int GS, bool NT = true>
-    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
+    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r, __amdgpu_buffer_rsrc_t rs,
+                            uint32_t lane, int u) {
         if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
 #pragma unroll
             for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
@@ -553,7 +585,7 @@ struct FxNvfp4 {
             r.s0 = ld_u32(sp);
             r.s1 = ld_u32(sp + 4);
         } else {
-            uint4 q = ld_codes_u128<NT>(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_code_chunk<NT>(rs, lane, u);
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
             const uint8_t* sp = w.codes + (o.s + (uint32_t)c * 128u);
             r.s0 = ld_u32(sp);
@@ -625,7 +657,7 @@ struct FxNvfp4 {
 template <int LAYOUT>
 struct FxQ4K {
     static constexpr int FMT = TITAN_Q4_K, CHUNK_COLS = 128;
-    static constexpr bool HAS_MFMA = true, PIPE = true, LAST_CACHED = false;
+    static constexpr bool HAS_MFMA = true, PIPE = true;
     // one token: fewer, longer waves (the 14336-column rows split over two
     // waves, not four) measured 2-5% faster on the Llama-3-8B layer (31.7 ->
     // 30.5 us); INT4 measured slower with the same target
@@ -641,7 +673,8 @@ struct FxQ4K {
             return {(uint32_t)tiled_code_off(g, row, 0, j), (uint32_t)tiled_q4k_hdr_off(g, row, 0)};
     }
     template <int GS, bool NT = true>
-    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
+    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r, __amdgpu_buffer_rsrc_t rs,
+                            uint32_t lane, int u) {
         const uint32_t blk = (uint32_t)c >> 1;
         if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
             r.hdr = ld_u128(w.codes + (o.h + blk * 144u));
@@ -650,7 +683,7 @@ struct FxQ4K {
             for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (q + 16u * i));
         } else {
             r.hdr = ld_u128(w.codes + (o.h + blk * 256u));
-            uint4 q = ld_codes_u128<NT>(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_code_chunk<NT>(rs, lane, u);
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
     }
@@ -800,6 +833,9 @@ struct FxQ3K {
     // the Llama-3-8B layer at one token (40.8 -> 35.5-36.0 us) and on
     // 28672x8192 at four tokens (58.5 -> 51.9 us), the other shapes unchanged
     static constexpr long long WAVES_TARGET = 1536;
+    // the EXACT kernel of this fold holds ~290 VGPRs against ~155 (one wave
+    // per SIMD instead of three): Q3_K keeps the general kernel
+    static constexpr bool NO_EXACT = true;
     // matrix cores: one 16x16x16 step per (word, level) = one 16-column
     // sub-block, folded at once with its scale (PIPE = false: issue and
     // finish of a chunk run back to back)
@@ -817,9 +853,10 @@ struct FxQ3K {
                 (uint32_t)tiled_q3k_sc_off(g, row, 0), (uint32_t)tiled_q3k_d_off(g, row, 0)};
     }
     template <int GS, bool NT = true>
-    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
+    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r, __amdgpu_buffer_rsrc_t rs,
+                            uint32_t lane, int u) {
         const uint32_t b = (uint32_t)c;
-        uint4 q = ld_codes_u128<NT>(w.codes + (o.c + b * 1024u));
+        uint4 q = ld_code_chunk<NT>(rs, lane, u);
         r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         const uint8_t* hp = w.codes + (o.h + b * 512u);
         r.hm0 = ld_u32(hp);
@@ -1026,12 +1063,13 @@ struct FxFp8 {
             return {(uint32_t)tiled_code_off(w.g, row, 0, j)};
     }
     template <int GS, bool NT = true>
-    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r) {
+    TQ_DEV static void load(const WDesc& w, const Off& o, int c, int, Raw& r, __amdgpu_buffer_rsrc_t rs,
+                            uint32_t lane, int u) {
         if constexpr (LAYOUT == TITAN_LAYOUT_REF) {
 #pragma unroll
             for (int i = 0; i < 4; i++) r.w[i] = ld_u32(w.codes + (o.c + (uint32_t)c * 64u + 16u * i));
         } else {
-            uint4 q = ld_codes_u128<NT>(w.codes + (o.c + (uint32_t)c * 1024u));
+            uint4 q = ld_code_chunk<NT>(rs, lane, u);
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
         }
     }

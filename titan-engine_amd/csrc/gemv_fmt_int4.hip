@@ -10,9 +10,3 @@ void dispatch_gemv_generic_int4(GemvArgs& a, int mcount, int rows, hipStream_t s
 }
 bool gemv_has_mfma_int4() { return fmt_has_mfma<TITAN_INT4>(); }
 }  // namespace tq
-
-#ifdef TQ_GEMV_TRACE
-extern "C" int titan_debug_gemv_trace(void* host, size_t bytes) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(tq::tq_gemv_trace), bytes);
-}
-#endif

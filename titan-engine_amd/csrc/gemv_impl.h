@@ -21,6 +21,12 @@
 
 namespace tq {
 
+// the kernels' helper lambdas carry register arrays by reference: they must
+// be inlined, or the arrays go to scratch memory
+#ifndef TQ_AI
+#define TQ_AI __attribute__((always_inline))
+#endif
+
 template <class F, class = void>
 struct has_stage_local : std::false_type {};
 template <class F>
@@ -31,15 +37,14 @@ template <class F>
 struct requires_sb_cell<F, std::void_t<decltype(F::SB_CELL)>> : std::true_type {};
 
 template <class F, class = void>
-struct has_last_cached : std::false_type {};
+struct has_no_exact : std::false_type {};
 template <class F>
-struct has_last_cached<F, std::void_t<decltype(F::LAST_CACHED)>> : std::true_type {};
-// Whether a wave loads its last weight group with cached loads (default) or,
-// like the others, nontemporal (LAST_CACHED = false: the branch between the
-// two measured slower than the refetch it saves)
+struct has_no_exact<F, std::void_t<decltype(F::NO_EXACT)>> : std::true_type {};
+// Whether one-phase launches take the EXACT kernel (a format may opt out when
+// that kernel's register allocation costs more than its simpler loop saves)
 template <class F>
-constexpr bool last_cached() {
-    if constexpr (has_last_cached<F>::value) return F::LAST_CACHED;
+constexpr bool allow_exact() {
+    if constexpr (has_no_exact<F>::value) return !F::NO_EXACT;
     else return true;
 }
 
@@ -277,12 +282,12 @@ TQ_DEV uint4 stage8_raw_of(uint4 v) {
     else return v;
 }
 
-#ifdef TQ_GEMV_TRACE
-// diagnostic build only: per-wave timestamps (100 MHz) and hardware ids
-static __device__ unsigned long long tq_gemv_trace[16384 * 4];
-#endif
 
-template <class F, int M, int MODE, int GS = 4>
+// EXACT: every problem of the launch has one phase whose groups cover its
+// chunks exactly (no chunk past the end of a row inside a group); the host
+// picks the kernel, so each kernel holds a single copy of the main loop (a
+// second copy in one kernel raised its register allocation by up to 2.5x)
+template <class F, int M, int MODE, int GS = 4, bool EXACT = false>
 __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     int bid = blockIdx.x, pi = 0;
@@ -314,6 +319,10 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
 
     const int row = tile * 16 + r;
     const typename F::Off off = F::base(W, row < rows ? row : rows - 1, j);  // past the end: not stored
+    // tiled code plane: this wave's tile, chunks [c0, c0 + nchunks) (a tile's
+    // chunk c sits at ((tile * chunks per row + c) * 64 + lane) * 16)
+    const CodeSrc csrc{W.codes + ((size_t)tile * (size_t)W.g.nchunks + (size_t)c0) * 1024u,
+                       (uint32_t)nchunks * 1024u, (uint32_t)lane * 16u};
 
     constexpr int NB = (M + 15) / 16;  // MFMA token blocks
     constexpr int NV = M < 4 ? M : 4;  // accumulator entries holding tokens
@@ -344,45 +353,32 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     // Each of the KS waves takes a contiguous quarter (half) of the phase, so
     // a group is U consecutive chunks starting at a multiple of U.
     const int pspan = pchunks >> ks_log;
-#ifndef TQ_GEMV_ROT
-#define TQ_GEMV_ROT 0
-#endif
-#if TQ_GEMV_ROT
-    // waves start their walk over a phase's groups at different groups
-    const int rot = (int)(((unsigned)tile * (unsigned)TQ_GEMV_ROT + (unsigned)pi * 5u + (unsigned)xpart * 3u) % (unsigned)gpp);
-    auto chunk_at = [&](int ph, int g, int u) {
-        int gg = g + rot;
-        gg = gg >= gpp ? gg - gpp : gg;
-        return ph * pchunks + part * pspan + gg * U + u;
-    };
-#else
-    auto chunk_at = [&](int ph, int g, int u) { return ph * pchunks + part * pspan + g * U + u; };
-#endif
-    // stream: nontemporal code loads.  For LAST_CACHED formats the wave's
-    // last group is loaded cached, so that the repeated loads past it (below)
-    // hit the cache instead of fetching the group from memory again.
-    auto load_group = [&](int ph, int g, typename F::Raw (&R)[U], bool stream) {
-        if (stream) {
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int cc = chunk_at(ph, g, u);
-                F::template load<GS, true>(W, off, c0 + (cc < nchunks ? cc : 0), j, R[u]);
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int cc = chunk_at(ph, g, u);
-                F::template load<GS, false>(W, off, c0 + (cc < nchunks ? cc : 0), j, R[u]);
-            }
-        }
+    auto chunk_at = [&](int ph, int g, int u) TQ_AI { return ph * pchunks + part * pspan + g * U + u; };
+    // Loop variants, as a compile-time tag: bit 0 = more than one phase,
+    // bit 1 = every chunk of every group lies inside the row (EXACT kernels),
+    // so no result needs a select.  The code plane is read through the
+    // wave's buffer resource with the chunk index unclamped (chunks past the
+    // row read zeros, without a memory access); the small scale / header
+    // planes are read with ordinary loads at a chunk clamped into the row.
+    auto in_row = [&](int cc) TQ_AI { return cc < nchunks ? cc : 0; };
+    // stream: nontemporal code loads (each byte is read once)
+    auto load_group = [&](int ph, int g, typename F::Raw (&R)[U]) TQ_AI {
+        // scale cells first: their decode is the first use of the group, and
+        // waiting for a load waits for every load issued before it
         if constexpr (has_sb_cell<F>()) {
             static_assert(U % GS == 0, "a chunk group holds whole scale cells");
 #pragma unroll
-            for (int u = 0; u < U; u += GS) {
-                const int cc = chunk_at(ph, g, u);
-                F::template load_cell<GS>(W, off, c0 + (cc < nchunks ? cc : 0), R[u]);
-            }
+            for (int u = 0; u < U; u += GS)
+                F::template load_cell<GS>(W, off, c0 + in_row(chunk_at(ph, g, u)), R[u]);
         }
+        // a group is U consecutive chunks: one resource, immediate offsets
+        const int cb = chunk_at(ph, g, 0);
+        const __amdgpu_buffer_rsrc_t rs = csrc.at(cb);
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            F::template load<GS, true>(W, off, c0 + in_row(cb + u), j, R[u], rs, csrc.lane, u);
+        // the group's loads go out before the fold of the previous group
+        __builtin_amdgcn_sched_barrier(0);
     };
     // One-round staging (fp16 activations): item e of a phase is token
     // e / nb8, columns [8 (e % nb8), +8); every load of a round is issued
@@ -394,11 +390,11 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     // the per-phase staging below).
     constexpr bool ONE = MODE != kModeF32 && (stage_local<F>() || M == 1);
     constexpr bool PERM = !stage_local<F>();
-    auto phase_cols = [&](int ph, int& col0, int& ncols) {
+    auto phase_cols = [&](int ph, int& col0, int& ncols) TQ_AI {
         col0 = (c0 + ph * pchunks) * F::CHUNK_COLS;
         ncols = min(pchunks * F::CHUNK_COLS, colend - col0);
     };
-    auto stage_issue = [&](int ph, int round, auto& S) {
+    auto stage_issue = [&](int ph, int round, auto& S) TQ_AI {
         constexpr int NI = sizeof(S.v) / sizeof(uint4);
         int col0, ncols;
         phase_cols(ph, col0, ncols);
@@ -415,7 +411,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             S.live |= live ? 1u << k : 0u;
         }
     };
-    auto stage_commit = [&](int ph, int round, const auto& S) {
+    auto stage_commit = [&](int ph, int round, const auto& S) TQ_AI {
         constexpr int NI = sizeof(S.v) / sizeof(uint4);
         int col0, ncols;
         phase_cols(ph, col0, ncols);
@@ -449,7 +445,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     };
     // raw rows -> the format's staged order, in place: every window a stage8
     // reads lies inside one round, so a round's reads precede its writes
-    auto stage_permute = [&](int ph) {
+    auto stage_permute = [&](int ph) TQ_AI {
         int col0, ncols;
         phase_cols(ph, col0, ncols);
         const int nb8 = ncols >> 3;
@@ -471,7 +467,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             __syncthreads();
         }
     };
-    auto stage_all = [&](int ph) {  // later phases: one round after another
+    auto stage_all = [&](int ph) TQ_AI {  // later phases: one round after another
         int col0, ncols;
         phase_cols(ph, col0, ncols);
         // (two items a round: this runs inside the main loop, where registers are scarce)
@@ -485,9 +481,13 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             stage_permute(ph);
         }
     };
-    auto fold_group = [&](int ph, int g, const typename F::Raw (&R)[U]) {
+    // multi_tag: whether the launch has more than one phase (only then can a
+    // group of a one-round-staging launch have to stage activations)
+    auto fold_group = [&](int ph, int g, const typename F::Raw (&R)[U], auto tag) TQ_AI {
+        constexpr bool MULTI = (decltype(tag)::value & 1) != 0;
+        constexpr bool EX = (decltype(tag)::value & 2) != 0;  // whole groups inside the row
         if constexpr (ONE) {
-            if (g == 0 && ph > 0) {  // phase 0 is staged before the main loop
+            if (MULTI && g == 0 && ph > 0) {  // phase 0 is staged before the main loop
                 __syncthreads();
                 stage_all(ph);
                 __syncthreads();
@@ -518,14 +518,16 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             // compiler unsure which loads have landed, and it would then drain
             // the next group's loads too): chunks past the end of the row fold
             // the staged columns of chunk 0 and are discarded by a select.
-            auto lbase_of = [&](int cc) { return cc < nchunks ? (cc - ph * pchunks) * F::CHUNK_COLS : 0; };
+            auto lbase_of = [&](int cc) TQ_AI {
+                return EX || cc < nchunks ? (cc - ph * pchunks) * F::CHUNK_COLS : 0;
+            };
             auto fold_into = [&](const typename F::template Tmp<NB, GS, SX>& T, const typename F::Dec& dec,
-                                 int cc, int lbase) {
+                                 int cc, int lbase) TQ_AI {
                 f4_t m2[NB];
 #pragma unroll
                 for (int n = 0; n < NB; n++) m2[n] = macc[n];
                 F::template finish<NB, NV, GS, SX>(T, dec, s16 + 4 * (lbase >> 5), m2);
-                const bool live = cc < nchunks;
+                const bool live = EX || cc < nchunks;
 #pragma unroll
                 for (int n = 0; n < NB; n++) macc[n] = live ? m2[n] : macc[n];
             };
@@ -591,35 +593,40 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     // (floor((2^32 - 1) / gpp)) is short by at most one for q < 2^31, and one
     // correction step makes the quotient exact
     const uint32_t gmag = 0xFFFFFFFFu / (uint32_t)gpp;
-    auto split_q = [&](int q, int& p, int& g) {
+    auto split_q = [&](int q, int& p, int& g) TQ_AI {
         uint32_t pq = __umulhi((uint32_t)q, gmag);
         uint32_t rq = (uint32_t)q - pq * (uint32_t)gpp;
         if (rq >= (uint32_t)gpp) { pq++; rq -= (uint32_t)gpp; }
         p = (int)pq;
         g = (int)rq;
     };
-    auto load_q = [&](int q, typename F::Raw (&R)[U]) {
-        const bool stream = !last_cached<F>() || q < ngroups - 1;
-        q = q < ngroups ? q : ngroups - 1;
-        int p, g;
-        split_q(q, p, g);
-        load_group(p, g, R, stream);
+    // single phase (tag bit 0 clear): group q is group q of phase 0
+    auto split_qm = [&](int q, int& p, int& g, auto tag) TQ_AI {
+        if constexpr ((decltype(tag)::value & 1) != 0) split_q(q, p, g);
+        else { p = 0; g = q; }
     };
-    auto fold_q = [&](int q, const typename F::Raw (&R)[U]) {
+    // Loads past the last group (the pipeline runs DEPTH - 1 groups ahead)
+    // address phase nph, i.e. chunks past the end of the row: they read
+    // zeros and fetch nothing.
+    auto load_q = [&](int q, typename F::Raw (&R)[U], auto tag) TQ_AI {
         int p, g;
-        split_q(q, p, g);
-        fold_group(p, g, R);
+        if (q < ngroups) split_qm(q, p, g, tag);
+        else { p = nph; g = 0; }
+        load_group(p, g, R);
     };
-#ifdef TQ_GEMV_TRACE
-    const unsigned long long tr0 = __builtin_amdgcn_s_memrealtime();
-    unsigned long long tr_a = 0;
-#endif
+    using kMulti = std::integral_constant<int, 1>;
+    using kExact = std::integral_constant<int, 2>;
+    auto fold_q = [&](int q, const typename F::Raw (&R)[U], auto tag) TQ_AI {
+        int p, g;
+        split_qm(q, p, g, tag);
+        fold_group(p, g, R, tag);
+    };
     if constexpr (ONE) {
         // the activations' loads go out ahead of the first weights
         XStage<kStageItems> S;
         stage_issue(0, 0, S);
 #pragma unroll
-        for (int d = 0; d < DEPTH - 1; d++) load_q(d, rbuf[d]);
+        for (int d = 0; d < DEPTH - 1; d++) load_q(d, rbuf[d], kMulti{});
         stage_commit(0, 0, S);
         int col0, ncols;
         phase_cols(0, col0, ncols);
@@ -635,23 +642,25 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
         __syncthreads();
     } else {
 #pragma unroll
-        for (int d = 0; d < DEPTH - 1; d++) load_q(d, rbuf[d]);
+        for (int d = 0; d < DEPTH - 1; d++) load_q(d, rbuf[d], kMulti{});
     }
-    for (int n = 0; n < ngroups; n += DEPTH) {
+    // Main loop.  The in-loop staging of later phases (multi-phase kernels
+    // only) is a branch whose loads and barriers make the compiler drain the
+    // next group's loads before each fold; EXACT kernels (one phase) have no
+    // such branch, so the next group's loads stay in flight under the fold.
+    auto main_loop = [&](auto tag) TQ_AI {
+        for (int n = 0; n < ngroups; n += DEPTH) {
 #pragma unroll
-        for (int d = 0; d < DEPTH; d++) {
-            if (n + d >= ngroups) break;
-            load_q(n + d + DEPTH - 1, rbuf[(d + DEPTH - 1) % DEPTH]);
-            fold_q(n + d, rbuf[d]);
-#ifdef TQ_GEMV_TRACE
-            if (n + d == 0) tr_a = __builtin_amdgcn_s_memrealtime();
-#endif
+            for (int d = 0; d < DEPTH; d++) {
+                if (n + d >= ngroups) break;
+                load_q(n + d + DEPTH - 1, rbuf[(d + DEPTH - 1) % DEPTH], tag);
+                fold_q(n + d, rbuf[d], tag);
+            }
         }
-    }
+    };
+    if constexpr (EXACT) main_loop(kExact{});
+    else main_loop(kMulti{});
 
-#ifdef TQ_GEMV_TRACE
-    const unsigned long long tr1 = __builtin_amdgcn_s_memrealtime();
-#endif
     // per-lane results: MFMA lane (r, q = j) holds tokens 16n + 4j + v of row
     // r; VALU lanes hold partial sums of row r over their words.
     float res[M];
@@ -752,21 +761,6 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
             }
         }
     }
-#ifdef TQ_GEMV_TRACE
-    {
-        unsigned hw, xcc;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-        const int wid = blockIdx.x * kGemvWaves + wave;
-        if (lane == 0 && wid < 16384) {
-            unsigned long long* t = tq_gemv_trace + 4 * wid;
-            t[0] = tr0;
-            t[1] = tr1;
-            t[2] = __builtin_amdgcn_s_memrealtime();
-            t[3] = ((unsigned long long)(pi | (part << 8) | ((xcc & 15) << 16) | ((unsigned)((tr_a - tr0) / 10 < 255ull ? (tr_a - tr0) / 10 : 255ull) << 24)) << 32) | hw;
-        }
-    }
-#endif
 }
 
 // ---- generic fallback for shapes the fast kernel does not take ------------------
@@ -922,12 +916,30 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
               << b.p[i].xs_log;
     }
     if constexpr (MODE == kModeMfma) {
-        if (gsteps == 4)
-            hipLaunchKernelGGL((qgemv_kernel<F, M, MODE, 4>), dim3(wg), dim3(kGemvThreads), lds, st, b);
-        else if (gsteps == 2)
-            hipLaunchKernelGGL((qgemv_kernel<F, M, MODE, 2>), dim3(wg), dim3(kGemvThreads), lds, st, b);
-        else
-            hipLaunchKernelGGL((qgemv_kernel<F, M, MODE, 1>), dim3(wg), dim3(kGemvThreads), lds, st, b);
+        // EXACT kernel: every problem folds its chunks in one phase of whole
+        // groups (the kernel's pchunks == its workgroup's chunk count)
+        bool exact = allow_exact<F>();
+        for (int i = 0; i < a.n; i++) {
+            const int nch = a.p[i].nchunks >> a.p[i].xs_log;
+            const int rnd = gemv_u<F, M, MODE>() << a.p[i].ks_log;
+            const int full = (nch + rnd - 1) / rnd * rnd;
+            const int pch = a.pc / F::CHUNK_COLS < full ? a.pc / F::CHUNK_COLS : full;
+            exact = exact && pch == nch;
+        }
+        auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(wg), dim3(kGemvThreads), lds, st, b); };
+        if constexpr (allow_exact<F>()) {
+            if (exact) {
+                if (gsteps == 4) go(qgemv_kernel<F, M, MODE, 4, true>);
+                else if (gsteps == 2) go(qgemv_kernel<F, M, MODE, 2, true>);
+                else go(qgemv_kernel<F, M, MODE, 1, true>);
+                return;
+            }
+        }
+        {
+            if (gsteps == 4) go(qgemv_kernel<F, M, MODE, 4, false>);
+            else if (gsteps == 2) go(qgemv_kernel<F, M, MODE, 2, false>);
+            else go(qgemv_kernel<F, M, MODE, 1, false>);
+        }
     } else {
         constexpr bool grouped = F::FMT == TITAN_INT4 || F::FMT == TITAN_INT2 || F::FMT == TITAN_FP4;
         if (grouped && gsteps == 1)
@@ -951,7 +963,8 @@ void launch_fast(GemvArgs& a, int mcount, int mode, int total_tiles, hipStream_t
             else if (mcount <= 4) launch_mode<F, 4, kModeMfma>(a, total_tiles, st);
             else if (mcount <= 8) launch_mode<F, 8, kModeMfma>(a, total_tiles, st);
             else if (mcount <= 16) launch_mode<F, 16, kModeMfma>(a, total_tiles, st);
-            else launch_mode<F, 32, kModeMfma>(a, total_tiles, st);
+            // 256-column chunks take at most 16 tokens a launch (run_gemv)
+            else if constexpr (F::CHUNK_COLS <= 128) launch_mode<F, 32, kModeMfma>(a, total_tiles, st);
         }
     } else if (mode == kModeDot2) {
         if (mcount == 1) launch_mode<F, 1, kModeDot2>(a, total_tiles, st);
