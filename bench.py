@@ -324,7 +324,7 @@ def cpu_baseline(layer, budget_s=12.0):
                       f"{el:.1f} s, {'AVX-512' if R is not None and R.variant == 'avx512' else 'scalar'} "
                       f"build of matmul_avx.cpp, 1 thread")
     # the same loop shape over all host cores (row-partitioned restatement)
-    nth = min(os.cpu_count() or 1, 64)
+    nth = cpu_threads()
     t0 = time.perf_counter()
     mt_passes = 0
     while True:
@@ -360,9 +360,23 @@ def cpu_gemv_baseline(fmt, ref, g, gs, rows, cols, nbytes, budget_s=1.0):
     x = np.random.default_rng(1).normal(0, 1, cols).astype(np.float32)
     passes, el = cpu_time(lambda: O.matvec_fmt_mt(fmt, codes, sc, bi, g, gs, x, rows, cols, 1),
                           budget_s)
-    return dict(value=round(nbytes * passes / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
-                sample=f"{passes} pass(es) of the {rows}x{cols} {fmt} GEMV, M=1 fp32 x, "
-                       f"{el:.2f} s, oracle restatement of the matmul_avx.cpp loop")
+    one = dict(value=round(nbytes * passes / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
+               sample=f"{passes} pass(es) of the {rows}x{cols} {fmt} GEMV, M=1 fp32 x, "
+                      f"{el:.2f} s, oracle restatement of the matmul_avx.cpp loop")
+    # the same loop with rows partitioned over the host threads
+    # (execute_experts_parallel's thread-per-task model, expert_cpu.cpp:39-102)
+    nth = cpu_threads()
+    passes, el = cpu_time(lambda: O.matvec_fmt_mt(fmt, codes, sc, bi, g, gs, x, rows, cols, nth),
+                          budget_s / 2)
+    allc = dict(value=round(nbytes * passes / el / 1e9, 3), unit="GB/s", cores=nth, kind="port",
+                sample=f"{passes} pass(es), rows partitioned over {nth} pthreads, {el:.2f} s")
+    return one, allc
+
+
+def cpu_threads():
+    """Host threads for the all-cores baselines: every core, at most the 16
+    cores a one-GPU box grants this job."""
+    return max(1, min(os.cpu_count() or 1, 16))
 
 
 def cpu_moe_baseline(mats, route, hidden, inter, budget_s=2.0):
@@ -529,8 +543,9 @@ def main():
                               ms=round(r["ms"], 5), GBps=round(r["gbs"], 1),
                               frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4)))
         if not args.no_cpu:
-            secondary[-1]["cpu_baseline"] = cpu_gemv_baseline("q4k", r["ref"], 0.0, 0, 4096, 4096,
-                                                              r["bytes"])
+            (secondary[-1]["cpu_baseline"],
+             secondary[-1]["cpu_baseline_all_cores"]) = cpu_gemv_baseline("q4k", r["ref"], 0.0, 0, 4096,
+                                                                          4096, r["bytes"])
         for M in (1, 4):
             for n, k in LLAMA70B:
                 log(f"Q3_K / INT2 {n}x{k} M={M}")
@@ -539,15 +554,17 @@ def main():
                                       ms=round(r["ms"], 5), GBps=round(r["gbs"], 1),
                                       frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4)))
                 if M == 1 and not args.no_cpu:
-                    secondary[-1]["cpu_baseline"] = cpu_gemv_baseline("q3k", r["ref"], 0.0, 0, n, k,
-                                                                      r["bytes"], budget_s=0.5)
+                    (secondary[-1]["cpu_baseline"],
+                     secondary[-1]["cpu_baseline_all_cores"]) = cpu_gemv_baseline(
+                        "q3k", r["ref"], 0.0, 0, n, k, r["bytes"], budget_s=0.5)
                 r = bench_int2(n, k, M, gen, max(20, K // 2), 5)
                 secondary.append(dict(config=f"INT2 g64 {n}x{k} GEMV", M=M, ms=round(r["ms"], 5),
                                       GBps=round(r["gbs"], 1),
                                       frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4)))
                 if M == 1 and not args.no_cpu:
-                    secondary[-1]["cpu_baseline"] = cpu_gemv_baseline("int2", r["ref"], 0.0, 64, n, k,
-                                                                      r["bytes"], budget_s=0.5)
+                    (secondary[-1]["cpu_baseline"],
+                     secondary[-1]["cpu_baseline_all_cores"]) = cpu_gemv_baseline(
+                        "int2", r["ref"], 0.0, 64, n, k, r["bytes"], budget_s=0.5)
                 torch.cuda.empty_cache()
         ex = None
         for T in (64, 1024):
