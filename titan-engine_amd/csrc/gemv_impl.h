@@ -273,6 +273,38 @@ constexpr bool stage_local() {
     if constexpr (has_stage_local<F>::value) return F::STAGE_LOCAL;
     else return false;
 }
+// Item e of a staging round: token m, 8-column group d of a row of nb8 groups
+// (one token: no division)
+template <int M>
+TQ_DEV void item_of_m(int e, int nb8, int& m, int& d) {
+    if constexpr (M == 1) {
+        m = e < nb8 ? 0 : 1;
+        d = e;
+    } else {
+        m = e / nb8;
+        d = e - m * nb8;
+    }
+}
+// Sum over the WL lanes ending at this lane within its DPP row of 16 (lanes
+// before the row's start count 0): Hillis-Steele steps of row shifts.
+template <int N>
+TQ_DEV float row_shr_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x110 + N, 0xF, 0xF, true));
+}
+template <int WL>
+TQ_DEV float row_window_sum(float v) {
+    if constexpr (WL >= 2) v += row_shr_f<1>(v);
+    if constexpr (WL >= 4) v += row_shr_f<2>(v);
+    if constexpr (WL >= 8) v += row_shr_f<4>(v);
+    if constexpr (WL >= 16) v += row_shr_f<8>(v);
+    if constexpr (WL >= 32) {
+        // row_bcast:15 with rows 1 and 3 written: the last lane of each odd
+        // row adds the even row's sum (rows 0 and 2 add 0)
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+    }
+    static_assert(WL <= 32, "a sum window spans at most two DPP rows");
+    return v;
+}
 constexpr int kStageItems = 8;  // 16-byte activation loads per thread and round
 template <int NI>
 struct XStage { uint4 v[NI]; unsigned live; };
@@ -353,7 +385,15 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     // Each of the KS waves takes a contiguous quarter (half) of the phase, so
     // a group is U consecutive chunks starting at a multiple of U.
     const int pspan = pchunks >> ks_log;
+#ifndef TQ_GEMV_KSI
+#define TQ_GEMV_KSI 0
+#endif
+#if TQ_GEMV_KSI
+    // waves of a tile interleave whole groups: wave part takes groups part, part + KS, ...
+    auto chunk_at = [&](int ph, int g, int u) TQ_AI { return ph * pchunks + ((g << ks_log) + part) * U + u; };
+#else
     auto chunk_at = [&](int ph, int g, int u) TQ_AI { return ph * pchunks + part * pspan + g * U + u; };
+#endif
     // Loop variants, as a compile-time tag: bit 0 = more than one phase,
     // bit 1 = every chunk of every group lies inside the row (EXACT kernels),
     // so no result needs a select.  The code plane is read through the
@@ -394,6 +434,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
         col0 = (c0 + ph * pchunks) * F::CHUNK_COLS;
         ncols = min(pchunks * F::CHUNK_COLS, colend - col0);
     };
+    auto item_of = [&](int e, int nb8, int& m, int& d) TQ_AI { item_of_m<M>(e, nb8, m, d); };
     auto stage_issue = [&](int ph, int round, auto& S) TQ_AI {
         constexpr int NI = sizeof(S.v) / sizeof(uint4);
         int col0, ncols;
@@ -404,7 +445,8 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int k = 0; k < NI; k++) {
             const int e = round + k * kGemvThreads + tid;
-            const int m = e / nb8, d = e - m * nb8;
+            int m, d;
+            item_of(e, nb8, m, d);
             const bool live = m < M && m < a.mcount;
             const int64_t src = live ? (int64_t)(a.m0 + m) * P.ldx + col0 + 8 * d : (int64_t)a.m0 * P.ldx + col0;
             S.v[k] = *(const uint4*)(xb + src);
@@ -419,24 +461,20 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int k = 0; k < NI; k++) {
             const int e = round + k * kGemvThreads + tid;
-            const int m = e / nb8, d = e - m * nb8;
+            int m, d;
+            item_of(e, nb8, m, d);
             const uint4 v = (S.live >> k) & 1u ? S.v[k] : make_uint4(0, 0, 0, 0);
             if (m < M) *(uint4*)(xh + m * pc + 8 * d) = PERM ? v : stage8_raw_of<F>(v);
             if constexpr (SX || MODE == kModeDot2) {
                 // SX: sums over one scale window at s16[sx_index(col / window, token)];
-                // VALU fold: sums over 16 columns at s16[token * (pc / 16) + col / 16]
+                // VALU fold: sums over 16 columns at s16[token * (pc / 16) + col / 16].
+                // The WL items of a window are WL consecutive lanes (one DPP
+                // row, or two for 32: nb8 and the rounds are multiples of WL
+                // items): the window's last lane holds its sum.
                 constexpr int SW = SX ? F::template sx_cols<GS>() : 16, WL = SW / 8;
-                const h8_t h = h8_of(v);
-                float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 8; i += 2) {
-                    a0 += (float)h[i];
-                    a1 += (float)h[i + 1];
-                }
-                float sum = a0 + a1;
-#pragma unroll
-                for (int o = 1; o < WL; o <<= 1) sum += __shfl_xor(sum, o, kWave);
-                if (m < M && d % WL == 0) {
+                float sum = dot2(v.x, kOnes2, dot2(v.y, kOnes2, 0.0f)) + dot2(v.z, kOnes2, dot2(v.w, kOnes2, 0.0f));
+                sum = row_window_sum<WL>(sum);
+                if (m < M && d % WL == WL - 1) {
                     if constexpr (SX) s16[sx_index<SW>(8 * d / SW, m)] = sum;
                     else s16[m * (pc >> 4) + d / 2] = sum;
                 }
@@ -454,14 +492,16 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int k = 0; k < 2; k++) {
                 const int e = round + k * kGemvThreads + tid;
-                const int m = e / nb8, d = e - m * nb8;
+                int m, d;
+                item_of(e, nb8, m, d);
                 o[k] = m < M ? F::stage8(xh + m * pc, 8 * d) : make_uint4(0, 0, 0, 0);
             }
             __syncthreads();
 #pragma unroll
             for (int k = 0; k < 2; k++) {
                 const int e = round + k * kGemvThreads + tid;
-                const int m = e / nb8, d = e - m * nb8;
+                int m, d;
+                item_of(e, nb8, m, d);
                 if (m < M) *(uint4*)(xh + m * pc + 8 * d) = o[k];
             }
             __syncthreads();
