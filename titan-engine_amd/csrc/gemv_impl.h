@@ -385,15 +385,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     // Each of the KS waves takes a contiguous quarter (half) of the phase, so
     // a group is U consecutive chunks starting at a multiple of U.
     const int pspan = pchunks >> ks_log;
-#ifndef TQ_GEMV_KSI
-#define TQ_GEMV_KSI 0
-#endif
-#if TQ_GEMV_KSI
-    // waves of a tile interleave whole groups: wave part takes groups part, part + KS, ...
-    auto chunk_at = [&](int ph, int g, int u) TQ_AI { return ph * pchunks + ((g << ks_log) + part) * U + u; };
-#else
     auto chunk_at = [&](int ph, int g, int u) TQ_AI { return ph * pchunks + part * pspan + g * U + u; };
-#endif
     // Loop variants, as a compile-time tag: bit 0 = more than one phase,
     // bit 1 = every chunk of every group lies inside the row (EXACT kernels),
     // so no result needs a select.  The code plane is read through the
