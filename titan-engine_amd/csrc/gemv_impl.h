@@ -99,13 +99,11 @@ constexpr int kGemvThreads = kGemvWaves * kWave;
 #ifndef TQ_GEMV_LDS_KB
 #define TQ_GEMV_LDS_KB 32
 #endif
-#ifndef TQ_GEMV_DEPTH
-#define TQ_GEMV_DEPTH 2  // weight groups in flight + 1
-#endif
 #ifndef TQ_GEMV_KS_MAX
 #define TQ_GEMV_KS_MAX 2
 #endif
 constexpr int kGemvLdsBytes = TQ_GEMV_LDS_KB * 1024;  // activation stage per workgroup
+constexpr int kGemvMaxLdsBytes = 96 * 1024;  // larger stage of small launches (dynamic LDS limit set)
 
 enum { kModeF32 = 0, kModeDot2 = 1, kModeMfma = 2 };
 
@@ -377,7 +375,6 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     const int pchunks = min(pc / F::CHUNK_COLS, (nchunks + round - 1) / round * round);
     const int gpp = pchunks / round;                // groups per phase per wave
     const int nph = (nchunks + pchunks - 1) / pchunks;
-    const int ngroups = nph * gpp;
 
     // group q = ph * gpp + g: chunks ph * pchunks + (g * U + u) * KS + part.
     // Groups are visited in order; the phase of a group is tracked
@@ -516,26 +513,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     // multi_tag: whether the launch has more than one phase (only then can a
     // group of a one-round-staging launch have to stage activations)
     auto fold_group = [&](int ph, int g, const typename F::Raw (&R)[U], auto tag) TQ_AI {
-        constexpr bool MULTI = (decltype(tag)::value & 1) != 0;
         constexpr bool EX = (decltype(tag)::value & 2) != 0;  // whole groups inside the row
-        if constexpr (ONE) {
-            if (MULTI && g == 0 && ph > 0) {  // phase 0 is staged before the main loop
-                __syncthreads();
-                stage_all(ph);
-                __syncthreads();
-            }
-        } else if (g == 0) {  // first group of a phase: stage its activations
-            const int col0 = (c0 + ph * pchunks) * F::CHUNK_COLS;
-            const int ncols = min(pchunks * F::CHUNK_COLS, colend - col0);
-            __syncthreads();
-            if constexpr (MODE == kModeF32)
-                stage_f32<M>(xf, s16, pc, P.x, a.xdt, P.ldx, a.m0, a.mcount, col0, ncols, tid);
-            else
-                stage_f16<F, M, MODE == kModeDot2>(xh, s16, pc, P.x, P.ldx, a.m0, a.mcount, col0, ncols, tid);
-            if constexpr (SX)
-                stage_sums<M, F::template sx_cols<GS>()>(s16, P.x, P.ldx, a.m0, a.mcount, col0, ncols, tid);
-            __syncthreads();
-        }
         if constexpr (MODE == kModeMfma) {
             // chunk u's MFMAs are issued before chunk u-1 is scaled
             const _Float16* xt[NB];
@@ -615,50 +593,26 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
         }
     };
 
-    // Weights of the next DEPTH - 1 groups are in flight while a group is
-    // folded.  Past the last group the loads repeat the last group (cache
-    // hits): unconditional loads keep the compiler's waits exact.
-    constexpr int DEPTH = TQ_GEMV_DEPTH;
-    static_assert(DEPTH == 2 || DEPTH == 3, "load depth");
-    typename F::Raw rbuf[DEPTH][U];
-    // q / gpp without a division per group: a reciprocal under-estimate
-    // (floor((2^32 - 1) / gpp)) is short by at most one for q < 2^31, and one
-    // correction step makes the quotient exact
-    const uint32_t gmag = 0xFFFFFFFFu / (uint32_t)gpp;
-    auto split_q = [&](int q, int& p, int& g) TQ_AI {
-        uint32_t pq = __umulhi((uint32_t)q, gmag);
-        uint32_t rq = (uint32_t)q - pq * (uint32_t)gpp;
-        if (rq >= (uint32_t)gpp) { pq++; rq -= (uint32_t)gpp; }
-        p = (int)pq;
-        g = (int)rq;
-    };
-    // single phase (tag bit 0 clear): group q is group q of phase 0
-    auto split_qm = [&](int q, int& p, int& g, auto tag) TQ_AI {
-        if constexpr ((decltype(tag)::value & 1) != 0) split_q(q, p, g);
-        else { p = 0; g = q; }
-    };
-    // Loads past the last group (the pipeline runs DEPTH - 1 groups ahead)
-    // address phase nph, i.e. chunks past the end of the row: they read
-    // zeros and fetch nothing.
-    auto load_q = [&](int q, typename F::Raw (&R)[U], auto tag) TQ_AI {
-        int p, g;
-        if (q < ngroups) split_qm(q, p, g, tag);
-        else { p = nph; g = 0; }
-        load_group(p, g, R);
-    };
+    // Two register sets of weights: the next group's loads are in flight
+    // while a group is folded.
+    typename F::Raw rbuf[2][U];
     using kMulti = std::integral_constant<int, 1>;
     using kExact = std::integral_constant<int, 2>;
-    auto fold_q = [&](int q, const typename F::Raw (&R)[U], auto tag) TQ_AI {
-        int p, g;
-        split_qm(q, p, g, tag);
-        fold_group(p, g, R, tag);
+    // Group (ph, g) with g possibly one past the phase's last group: the next
+    // phase's first group, or past the last phase chunks beyond the row,
+    // which read zeros and fetch nothing.
+    auto load_next = [&](int ph, int g, typename F::Raw (&R)[U]) TQ_AI {
+        if (g >= gpp) {
+            ph++;
+            g -= gpp;
+        }
+        load_group(ph, g, R);
     };
     if constexpr (ONE) {
         // the activations' loads go out ahead of the first weights
         XStage<kStageItems> S;
         stage_issue(0, 0, S);
-#pragma unroll
-        for (int d = 0; d < DEPTH - 1; d++) load_q(d, rbuf[d], kMulti{});
+        load_group(0, 0, rbuf[0]);
         stage_commit(0, 0, S);
         int col0, ncols;
         phase_cols(0, col0, ncols);
@@ -673,20 +627,43 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
         }
         __syncthreads();
     } else {
-#pragma unroll
-        for (int d = 0; d < DEPTH - 1; d++) load_q(d, rbuf[d], kMulti{});
+        load_group(0, 0, rbuf[0]);
     }
-    // Main loop.  The in-loop staging of later phases (multi-phase kernels
-    // only) is a branch whose loads and barriers make the compiler drain the
-    // next group's loads before each fold; EXACT kernels (one phase) have no
-    // such branch, so the next group's loads stay in flight under the fold.
+    // Activations of phase ph (the one-round staging has phase 0 staged
+    // above); between two phases, so no fold waits on its loads or barriers.
+    auto stage_phase = [&](int ph) TQ_AI {
+        __syncthreads();  // the previous phase's folds are done with the stage
+        if constexpr (ONE) {
+            stage_all(ph);
+        } else {
+            const int col0 = (c0 + ph * pchunks) * F::CHUNK_COLS;
+            const int ncols = min(pchunks * F::CHUNK_COLS, colend - col0);
+            if constexpr (MODE == kModeF32)
+                stage_f32<M>(xf, s16, pc, P.x, a.xdt, P.ldx, a.m0, a.mcount, col0, ncols, tid);
+            else
+                stage_f16<F, M, MODE == kModeDot2>(xh, s16, pc, P.x, P.ldx, a.m0, a.mcount, col0, ncols, tid);
+            if constexpr (SX)
+                stage_sums<M, F::template sx_cols<GS>()>(s16, P.x, P.ldx, a.m0, a.mcount, col0, ncols, tid);
+        }
+        __syncthreads();
+    };
+    // Main loop: phases outside, groups inside.  The inner loop holds no
+    // branch with loads or barriers, so the compiler keeps the next group's
+    // loads in flight under each fold (a staging branch inside it made the
+    // compiler drain them before every fold).  Register set 0 holds each
+    // phase's even groups: with more than one phase the host makes the group
+    // count per phase even, so the next phase's first group lands in set 0.
     auto main_loop = [&](auto tag) TQ_AI {
-        for (int n = 0; n < ngroups; n += DEPTH) {
-#pragma unroll
-            for (int d = 0; d < DEPTH; d++) {
-                if (n + d >= ngroups) break;
-                load_q(n + d + DEPTH - 1, rbuf[(d + DEPTH - 1) % DEPTH], tag);
-                fold_q(n + d, rbuf[d], tag);
+        constexpr bool MULTI = (decltype(tag)::value & 1) != 0;
+        const int nphl = MULTI ? nph : 1;
+        for (int ph = 0; ph < nphl; ph++) {
+            if (!ONE || ph > 0) stage_phase(ph);
+            for (int g = 0; g < gpp; g += 2) {
+                load_next(ph, g + 1, rbuf[1]);
+                fold_group(ph, g, rbuf[0], tag);
+                if (g + 1 >= gpp) break;
+                load_next(ph, g + 2, rbuf[0]);
+                fold_group(ph, g + 1, rbuf[1], tag);
             }
         }
     };
@@ -848,6 +825,12 @@ template <int L> struct Pick<TITAN_Q4_K, L> { using type = FxQ4K<L>; };
 template <int L> struct Pick<TITAN_Q3_K, L> { using type = FxQ3K<L>; };
 template <int L> struct Pick<TITAN_FP8_E4M3, L> { using type = FxFp8<L>; };
 
+// Lets a kernel take up to kGemvMaxLdsBytes of dynamic LDS (above the 64 KiB
+// default); setting it again is harmless.
+inline void set_max_lds(const void* kern) {
+    (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, kGemvMaxLdsBytes);
+}
+
 template <class F, int M, int MODE>
 void launch_mode(GemvArgs& a, int, hipStream_t st) {
     const int gsteps = a.p[0].gsteps;  // MFMA: word steps per scale group (same for all problems)
@@ -929,6 +912,45 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
     if (cap < step) cap = step;
     const int need = (maxcols + step - 1) / step * step;
     a.pc = need < cap ? need : cap;
+    // A problem folded in several phases needs an even number of groups per
+    // phase per wave (the kernel pairs groups in two register sets across
+    // phase boundaries).  A phase is a whole number of 4-wave rounds of U
+    // chunks, so a K split over at most two waves always gives an even count;
+    // a 4-wave split needs phases of an even number of rounds.  When the
+    // launch holds few workgroups per CU the stage doubles (the K split, and
+    // with it the wave count, stays); otherwise the split drops to two waves.
+    auto odd_phases = [&](int pcx) {
+        for (int i = 0; i < a.n; i++) {
+            const GemvProb& p = a.p[i];
+            const int nch = p.nchunks >> p.xs_log;
+            const int rnd = gemv_u<F, M, MODE>() << p.ks_log;
+            const int full = (nch + rnd - 1) / rnd * rnd;
+            const int pch = pcx / F::CHUNK_COLS < full ? pcx / F::CHUNK_COLS : full;
+            if ((nch + pch - 1) / pch > 1 && (pch / rnd) % 2 != 0) return true;
+        }
+        return false;
+    };
+    if (odd_phases(a.pc) && 2 * a.pc <= need) {
+        long long wgs = 0;
+        for (int i = 0; i < a.n; i++)
+            wgs += (long long)((a.p[i].ntiles + (kGemvWaves >> a.p[i].ks_log) - 1) /
+                               (kGemvWaves >> a.p[i].ks_log)) << a.p[i].xs_log;
+        const long long per_cu = (wgs + 255) / 256;
+        const size_t stage2 = (size_t)M * 2 * a.pc * per4 / 4 + (MODE == kModeMfma ? a.pc : 0) + 16;
+        if (stage2 <= kGemvMaxLdsBytes && (long long)stage2 * per_cu <= 160 * 1024) a.pc *= 2;
+    }
+    for (int i = 0; i < a.n; i++) {
+        GemvProb& p = a.p[i];
+        const int nch = p.nchunks >> p.xs_log;
+        for (;;) {
+            const int rnd = gemv_u<F, M, MODE>() << p.ks_log;
+            const int full = (nch + rnd - 1) / rnd * rnd;
+            const int pch = a.pc / F::CHUNK_COLS < full ? a.pc / F::CHUNK_COLS : full;
+            const int nph = (nch + pch - 1) / pch;
+            if (nph == 1 || (pch / rnd) % 2 == 0 || p.ks_log == 0) break;
+            p.ks_log--;
+        }
+    }
     const size_t stage = (size_t)M * a.pc * per4 / 4 + (MODE == kModeMfma ? a.pc / 2 : 0) + 16;
     const size_t red = (size_t)kGemvWaves * M * 16 * 4;
     const size_t lds = stage > red ? stage : red;
@@ -958,7 +980,10 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
             const int pch = a.pc / F::CHUNK_COLS < full ? a.pc / F::CHUNK_COLS : full;
             exact = exact && pch == nch;
         }
-        auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(wg), dim3(kGemvThreads), lds, st, b); };
+        auto go = [&](auto kern) {
+            if (lds > 64 * 1024) set_max_lds((const void*)kern);
+            hipLaunchKernelGGL(kern, dim3(wg), dim3(kGemvThreads), lds, st, b);
+        };
         if constexpr (allow_exact<F>()) {
             if (exact) {
                 if (gsteps == 4) go(qgemv_kernel<F, M, MODE, 4, true>);
@@ -974,12 +999,13 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
         }
     } else {
         constexpr bool grouped = F::FMT == TITAN_INT4 || F::FMT == TITAN_INT2 || F::FMT == TITAN_FP4;
-        if (grouped && gsteps == 1)
-            hipLaunchKernelGGL((qgemv_kernel<F, M, MODE, 1>), dim3(wg), dim3(kGemvThreads), lds, st, b);
-        else if (grouped && gsteps == 2)
-            hipLaunchKernelGGL((qgemv_kernel<F, M, MODE, 2>), dim3(wg), dim3(kGemvThreads), lds, st, b);
-        else
-            hipLaunchKernelGGL((qgemv_kernel<F, M, MODE, 4>), dim3(wg), dim3(kGemvThreads), lds, st, b);
+        auto go = [&](auto kern) {
+            if (lds > 64 * 1024) set_max_lds((const void*)kern);
+            hipLaunchKernelGGL(kern, dim3(wg), dim3(kGemvThreads), lds, st, b);
+        };
+        if (grouped && gsteps == 1) go(qgemv_kernel<F, M, MODE, 1>);
+        else if (grouped && gsteps == 2) go(qgemv_kernel<F, M, MODE, 2>);
+        else go(qgemv_kernel<F, M, MODE, 4>);
     }
 }
 
