@@ -569,7 +569,7 @@ def main():
         ex = None
         for T in (64, 1024):
             log(f"NVFP4 MoE T={T}")
-            r, ex = bench_moe(T, max(10, K // 10), 3, gen, ex)
+            r, ex = bench_moe(T, max(20, K // 10), 5, gen, ex)
             secondary.append(dict(config=f"NVFP4 MoE 256 experts top-8 7168/2048 T={T} "
                                          "(synthetic codes)", T=T, ms=round(r["ms"], 4),
                                   experts_hit=r["experts_hit"], GBps=round(r["gbs"], 1),
@@ -582,7 +582,8 @@ def main():
         torch.cuda.empty_cache()
         for (M, N, Kd) in [(2048, 14336, 4096), (2048, 4096, 14336)]:
             log(f"FP8 GEMM {M}x{N}x{Kd}")
-            r = bench_fp8(M, N, Kd, gen, max(10, K // 10), 3)
+            # steady state: the first launches after the MoE lines run cold
+            r = bench_fp8(M, N, Kd, gen, max(50, K // 4), 20)
             secondary.append(dict(config=f"FP8 E4M3 GEMM M={M} N={N} K={Kd} (+act quant)",
                                   ms=round(r["ms"], 4), TFLOPS=round(r["tflops"], 1),
                                   gemm_only_TFLOPS=round(r["gemm_tflops"], 1),
