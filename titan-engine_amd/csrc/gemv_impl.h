@@ -2,12 +2,14 @@
 //
 // Replaces the reference's one-block-per-row kernels (dequant.cu:23-172,
 // fp4.cu:28-84, fp4.cu:187-238).  Design for gfx950:
-//  * A workgroup of 4 waves owns RT tiles of 16 rows and the whole K range.
-//    The waves split K (wave w takes 64-byte chunks w, w+4, ...): the
-//    workgroup streams 256 contiguous code bytes per row at a time.
+//  * A workgroup of 4 waves owns up to 4 row tiles of 16 rows; waves that
+//    share a tile (K split) take contiguous spans of its 1 KiB chunks, and
+//    long rows may also be split across workgroups (caller workspace).
 //  * Each wave holds two groups of U chunks of codes in registers, so the
 //    next group's loads (4 KiB per wave) are in flight while the current one
-//    is folded; loads never depend on a branch.
+//    is folded; loads never depend on a branch, and the code plane is read
+//    through a buffer resource whose range check turns the loads past a
+//    wave's last group into zero-traffic reads.
 //  * Activations are staged per workgroup into LDS (phases of at most
 //    kGemvLdsBytes for long K / many tokens): fp32 in column order for fp32 /
 //    bf16 inputs, fp16 in each format's pairing order for fp16 inputs.
