@@ -345,3 +345,42 @@ def test_kquant_llama8b_layer_full_size(fmt, M):
         for t in sorted({0, M - 1}):
             ref = O.matvec_fmt_mt(fmt, b, None, None, 1.0, 0, X[k][t].float().cpu().numpy(), n, k, 8)
             assert_close_out(to_np(y[t]), ref.astype(np.float64), "f32")
+
+
+# chunk counts that end inside a group of 4 chunks (ragged), rows long enough
+# to need two activation phases at one token, and the doubled stage of small
+# multi-phase launches
+RAGGED = {"int4": [(48, 640, 128), (48, 17024, 128)], "int2": [(48, 1280, 64), (32, 17152, 64)],
+          "fp4": [(32, 640, 64)], "nvfp4": [(48, 640, 16), (32, 16512, 16)],
+          "q4k": [(32, 768, 256), (32, 16640, 256)], "q3k": [(32, 1280, 256), (16, 16640, 256)],
+          "fp8": [(32, 320, 0)]}
+
+
+@pytest.mark.parametrize("fmt,rows,cols,gs", [(f, r, c, g) for f, v in RAGGED.items() for r, c, g in v])
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_tiled_ragged_and_multi_phase(fmt, rows, cols, gs, M, rng):
+    """Rows whose chunks end inside a group (the loads past the row read zeros
+    through the code plane's range check and their results are discarded) and
+    rows folded in several activation phases, every tiled format, against the
+    fp64 product of the oracle's exact dequantized weights."""
+    d = make_weights(fmt, rows, cols, rng, gs=gs or 128)
+    W = upload(d, tq.LAYOUT_TILED)
+    x, x64 = act(M, cols, "f16", rng)
+    y = tq.qgemm(W, x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close_out(to_np(y), x64 @ d["deq"].astype(np.float64).T, "f32")
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_batched_exact_and_ragged_mix(M, rng):
+    """One batched launch whose problems are partly whole groups and partly
+    ragged (the launch takes the general kernel), with different K."""
+    shapes = [(64, 4096), (48, 640), (32, 2048), (16, 896)]
+    ds = [make_weights("int4", r, c, rng, gs=128) for r, c in shapes]
+    Ws = [upload(d, tq.LAYOUT_TILED) for d in ds]
+    X = [act(M, c, "f16", rng) for _, c in shapes]
+    Ys = [torch.zeros(M, r, dtype=torch.float32, device="cuda") for r, _ in shapes]
+    tq.qgemm_batched(Ws, [x for x, _ in X], Ys)
+    torch.cuda.synchronize()
+    for d, (_, x64), Y in zip(ds, X, Ys):
+        assert_close_out(to_np(Y), x64 @ d["deq"].astype(np.float64).T, "f32")
