@@ -131,6 +131,9 @@ struct GemvProb {
 };
 
 struct GemvArgs {
+    // first workgroup of each problem (ascending), INT_MAX past the last one:
+    // the kernel finds its problem from this one block of scalar loads
+    int wgb[TITAN_MAX_BATCH];
     GemvProb p[TITAN_MAX_BATCH];
     int n;
     int xdt, ydt;
@@ -322,9 +325,13 @@ TQ_DEV uint4 stage8_raw_of(uint4 v) {
 template <class F, int M, int MODE, int GS = 4, bool EXACT = false>
 __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    int bid = blockIdx.x, pi = 0;
-    for (int i = 1; i < a.n; i++)
-        if (bid >= a.p[i].wg_begin) pi = i;
+    // this workgroup's problem: a count over the first-workgroup table, with
+    // no chain of dependent scalar loads (a scan over the problems one by one
+    // took 2 us to issue the first load of a seven-problem launch)
+    const int bid = blockIdx.x;
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < TITAN_MAX_BATCH; i++) pi += bid >= a.wgb[i] ? 1 : 0;
     const GemvProb& P = a.p[pi];
     const WDesc& W = P.w;
     const int rows = W.g.rows;
@@ -964,10 +971,12 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
             int t = order[k2]; order[k2] = order[k2 - 1]; order[k2 - 1] = t;
         }
     GemvArgs b = a;
+    for (int i = 0; i < TITAN_MAX_BATCH; i++) b.wgb[i] = INT_MAX;
     int wg = 0;
     for (int i = 0; i < a.n; i++) {
         b.p[i] = a.p[order[i]];
         b.p[i].wg_begin = wg;
+        b.wgb[i] = wg;
         wg += (b.p[i].ntiles + (kGemvWaves >> b.p[i].ks_log) - 1) / (kGemvWaves >> b.p[i].ks_log)
               << b.p[i].xs_log;
     }
