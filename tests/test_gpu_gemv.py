@@ -384,3 +384,35 @@ def test_batched_exact_and_ragged_mix(M, rng):
     torch.cuda.synchronize()
     for d, (_, x64), Y in zip(ds, X, Ys):
         assert_close_out(to_np(Y), x64 @ d["deq"].astype(np.float64).T, "f32")
+
+
+@pytest.mark.parametrize("fmt,M", [("int2", 1), ("int2", 4), ("q3k", 1)])
+def test_tail_split_eight_problem_batch(fmt, M):
+    """Eight 2304 x 8192 problems in one launch: each takes a two-wave K split
+    (72 workgroups, 576 in all), so the last 64 workgroups, the tail of the
+    last problem, are re-split into one-tile workgroups and that problem into
+    two (nine problems in the launch).  Every output of the first and last
+    token against the oracle's fp32 GEMV of the same bytes."""
+    import bench
+    n, k = 2304, 8192
+    gen = torch.Generator(device="cuda").manual_seed(77 + M)
+    Ws, refs = [], []
+    for _ in range(8):
+        if fmt == "int2":
+            (m,) = bench.make_int4_layer(gen, gs=64, bits=2, shapes=[("w", n, k)])
+            Ws.append(tq.QWeight(tq.INT2, tq.LAYOUT_TILED, n, k, m["tiled"], group_size=64))
+            w, s, b = (t.cpu().numpy() for t in m["ref"])
+            refs.append((w.view(np.uint32), s.view(np.uint16), b.view(np.uint16), 64))
+        else:
+            blk = bench.random_kquant(tq.Q3_K, n, k, gen)
+            Ws.append(tq.QWeight(tq.Q3_K, tq.LAYOUT_TILED, n, k,
+                                 torch.from_numpy(tq.repack_host(tq.Q3_K, n, k, blk)).cuda()))
+            refs.append((blk, None, None, 0))
+    X = [torch.randn(M, k, generator=gen, device="cuda").half() for _ in range(8)]
+    Ys = [torch.empty(M, n, device="cuda", dtype=torch.float32) for _ in range(8)]
+    tq.qgemm_batched(Ws, X, Ys)
+    torch.cuda.synchronize()
+    for (codes, s16, b16, gs), x, y in zip(refs, X, Ys):
+        for t in sorted({0, M - 1}):
+            ref = O.matvec_fmt_mt(fmt, codes, s16, b16, 1.0, gs, x[t].float().cpu().numpy(), n, k, 8)
+            assert_close_out(to_np(y[t]), ref.astype(np.float64), "f32")

@@ -116,7 +116,8 @@ struct GemvProb {
     int64_t ldx, ldy;
     int nchunks;   // cols / CHUNK_COLS
     int wg_begin;  // first workgroup of this problem
-    int ntiles;    // ceil(rows / 16)
+    int ntiles;    // row tiles of this problem: [tile0, tile0 + ntiles)
+    int tile0;     // first row tile (0 unless the launch split the matrix's rows)
     int gsteps;    // MFMA word steps per scale group (power of two <= 4)
     int ks_log;    // log2 of the waves sharing one row tile (K split)
     // K split across workgroups (xs_log > 0 only with a caller workspace):
@@ -130,11 +131,14 @@ struct GemvProb {
     int* wsc;
 };
 
+// a launch holds the caller's problems plus at most one row split of one of them
+constexpr int kGemvMaxProbs = TITAN_MAX_BATCH + 1;
+
 struct GemvArgs {
     // first workgroup of each problem (ascending), INT_MAX past the last one:
     // the kernel finds its problem from this one block of scalar loads
-    int wgb[TITAN_MAX_BATCH];
-    GemvProb p[TITAN_MAX_BATCH];
+    int wgb[kGemvMaxProbs];
+    GemvProb p[kGemvMaxProbs];
     int n;
     int xdt, ydt;
     int m0;      // first token of this launch
@@ -331,7 +335,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     const int bid = blockIdx.x;
     int pi = 0;
 #pragma unroll
-    for (int i = 1; i < TITAN_MAX_BATCH; i++) pi += bid >= a.wgb[i] ? 1 : 0;
+    for (int i = 1; i < kGemvMaxProbs; i++) pi += bid >= a.wgb[i] ? 1 : 0;
     const GemvProb& P = a.p[pi];
     const WDesc& W = P.w;
     const int rows = W.g.rows;
@@ -344,7 +348,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     const int part = wave & (KS - 1);
     const int xs_log = P.xs_log, XS = 1 << xs_log;
     const int wgl = bid - P.wg_begin, xpart = wgl & (XS - 1), wgt = wgl >> xs_log;
-    const int tile = wgt * (kGemvWaves >> ks_log) + (wave >> ks_log);
+    const int tile = P.tile0 + wgt * (kGemvWaves >> ks_log) + (wave >> ks_log);
     const int pc = a.pc;
     // this workgroup's chunk range [c0, c0 + nchunks); chunk indices below
     // are relative to c0
@@ -841,7 +845,8 @@ inline void set_max_lds(const void* kern) {
 }
 
 template <class F, int M, int MODE>
-void launch_mode(GemvArgs& a, int, hipStream_t st) {
+void launch_mode(const GemvArgs& args, int, hipStream_t st) {
+    GemvArgs a = args;  // this launch's split and phase choices stay local
     const int gsteps = a.p[0].gsteps;  // MFMA: word steps per scale group (same for all problems)
     // K split per problem so that every wave folds a similar number of
     // chunks (long rows are shared by 2 or 4 waves); the wave count aimed for
@@ -906,6 +911,58 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
             }
         }
     }
+    // The last round of workgroups.  Workgroup b runs on XCD b % 8 and there
+    // on CU slot (b / 8) % 32 (round robin; the workgroups of these launches
+    // are resident together), so with a workgroup count that is not a multiple
+    // of the CU count, the last (count mod 256) workgroups are one more
+    // workgroup on only some of the CUs, and those CUs finish last.  For the
+    // 256-column-chunk formats the row tiles of those last workgroups get a
+    // K split of four waves instead (a workgroup of one row tile), which
+    // spreads them over every CU (INT2 28672 x 8192, one token: 19.7-20.2 ->
+    // 18.5 us).  For INT4 / Q4_K the small workgroups' fixed costs outweigh
+    // it (INT4 8B layer 22.7 -> 23.8 us).  The problem the tail begins in is
+    // split at a workgroup boundary into two problems.
+    if constexpr (F::CHUNK_COLS > 128) {
+        constexpr int kCUs = 256;
+        constexpr int U = gemv_u<F, M, MODE>();
+        bool xs = false;
+        for (int i = 0; i < a.n; i++) xs = xs || a.p[i].xs_log > 0;
+        int ord[kGemvMaxProbs];
+        for (int i = 0; i < a.n; i++) ord[i] = i;
+        for (int i = 1; i < a.n; i++)  // launch order: long rows first (stable)
+            for (int k2 = i; k2 > 0 && a.p[ord[k2]].nchunks > a.p[ord[k2 - 1]].nchunks; k2--) {
+                int t2 = ord[k2]; ord[k2] = ord[k2 - 1]; ord[k2 - 1] = t2;
+            }
+        auto wgs_of = [](const GemvProb& p) {
+            return (p.ntiles + (kGemvWaves >> p.ks_log) - 1) / (kGemvWaves >> p.ks_log);
+        };
+        long long nwg = 0;
+        for (int i = 0; i < a.n; i++) nwg += wgs_of(a.p[i]);
+        const int tail = (int)(nwg % kCUs);
+        if (!xs && a.n < kGemvMaxProbs && nwg > kCUs && tail > 0 && tail <= kCUs / 2) {
+            int left = tail;
+            for (int q = a.n - 1; q >= 0 && left > 0; q--) {
+                GemvProb& p = a.p[ord[q]];
+                // each wave keeps at least two groups of U chunks
+                const int ks2 = (p.nchunks >> TQ_GEMV_KS_MAX) >= 2 * U ? TQ_GEMV_KS_MAX : p.ks_log;
+                if (ks2 <= p.ks_log) break;
+                const int w = wgs_of(p);
+                if (w <= left) {
+                    p.ks_log = ks2;
+                    left -= w;
+                } else {
+                    const int keep = (w - left) * (kGemvWaves >> p.ks_log);  // tiles
+                    GemvProb s = p;
+                    s.tile0 = p.tile0 + keep;
+                    s.ntiles = p.ntiles - keep;
+                    s.ks_log = ks2;
+                    p.ntiles = keep;
+                    a.p[a.n++] = s;
+                    left = 0;
+                }
+            }
+        }
+    }
     // phase width: whole rounds of 4 waves x U = 4 chunks, at most
     // kGemvLdsBytes of staged activations (at least one round), no wider
     // than the longest row
@@ -964,14 +1021,14 @@ void launch_mode(GemvArgs& a, int, hipStream_t st) {
     const size_t red = (size_t)kGemvWaves * M * 16 * 4;
     const size_t lds = stage > red ? stage : red;
     // workgroups: long-K problems first (they take longest)
-    int order[TITAN_MAX_BATCH];
+    int order[kGemvMaxProbs];
     for (int i = 0; i < a.n; i++) order[i] = i;
     for (int i = 1; i < a.n; i++)
         for (int k2 = i; k2 > 0 && a.p[order[k2]].nchunks > a.p[order[k2 - 1]].nchunks; k2--) {
             int t = order[k2]; order[k2] = order[k2 - 1]; order[k2 - 1] = t;
         }
     GemvArgs b = a;
-    for (int i = 0; i < TITAN_MAX_BATCH; i++) b.wgb[i] = INT_MAX;
+    for (int i = 0; i < kGemvMaxProbs; i++) b.wgb[i] = INT_MAX;
     int wg = 0;
     for (int i = 0; i < a.n; i++) {
         b.p[i] = a.p[order[i]];
