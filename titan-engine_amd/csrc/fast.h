@@ -364,6 +364,10 @@ struct FxInt2 {
     // faster on 28672x8192 at four tokens (42.6 -> 33.2 us), the other shapes
     // unchanged; one token keeps 2048 (28672x8192 1.5% slower with 1536)
     static constexpr long long WAVES_TARGET = 1536, WAVES_TARGET_M1 = 2048;
+    // several tokens, rows in several activation phases: at most two waves a
+    // row tile (8192 x 28672 at four tokens 47.6-49.3 -> 45.2 us, 8192 x 8192
+    // 17.4 -> 16.1 us; one token and small launches keep the wider split)
+    static constexpr bool KS1_MULTI_PHASE = true;
     static constexpr bool SB_CELL = LAYOUT == TITAN_LAYOUT_TILED;
     struct Off { uint32_t c, s, b; };
     struct Raw { uint32_t w[4], s[4], b[4]; uint4 q; };

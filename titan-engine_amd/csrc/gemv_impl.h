@@ -72,6 +72,16 @@ constexpr long long waves_target() {
 }
 
 template <class F, class = void>
+struct has_ks1_mp : std::false_type {};
+template <class F>
+struct has_ks1_mp<F, std::void_t<decltype(F::KS1_MULTI_PHASE)>> : std::true_type {};
+template <class F>
+constexpr bool has_ks1_multi_phase() {
+    if constexpr (has_ks1_mp<F>::value) return F::KS1_MULTI_PHASE;
+    else return false;
+}
+
+template <class F, class = void>
 struct has_sx_max_m : std::false_type {};
 template <class F>
 struct has_sx_max_m<F, std::void_t<decltype(F::SX_MAX_M)>> : std::true_type {};
@@ -998,6 +1008,25 @@ void launch_mode(const GemvArgs& args, int, hipStream_t st) {
         }
         return false;
     };
+    // Formats that fold several tokens best with at least two groups per wave
+    // and phase (KS1_MULTI_PHASE): rows folded in several phases split over
+    // at most two waves, while the launch keeps 1024 waves or more.  Decided
+    // before the stage doubling below: two phases at two waves measured
+    // faster than one doubled phase at four (INT2 8192 x 8192, four tokens).
+    if constexpr (M > 1 && has_ks1_multi_phase<F>()) {
+        long long waves = 0, capped = 0;
+        for (int i = 0; i < a.n; i++) {
+            const GemvProb& p = a.p[i];
+            const bool multi = (long long)(p.nchunks >> p.xs_log) * F::CHUNK_COLS > a.pc;
+            waves += (long long)p.ntiles << p.ks_log;
+            capped += (long long)p.ntiles << (multi && p.ks_log > 1 ? 1 : p.ks_log);
+        }
+        if (capped < waves && capped >= 1024)
+            for (int i = 0; i < a.n; i++) {
+                GemvProb& p = a.p[i];
+                if ((long long)(p.nchunks >> p.xs_log) * F::CHUNK_COLS > a.pc && p.ks_log > 1) p.ks_log = 1;
+            }
+    }
     if (odd_phases(a.pc) && 2 * a.pc <= need) {
         long long wgs = 0;
         for (int i = 0; i < a.n; i++)
