@@ -60,10 +60,43 @@ def test_repack_roundtrip_bytes(fmt, rows, cols, rng):
         assert np.array_equal(s2, scales)
     if biases is not None:
         assert np.array_equal(b2, biases)
-    # a permutation: the multiset of bytes is unchanged
+    # a permutation: the multiset of bytes is unchanged -- except Q3_K, whose
+    # tiled hmask words permute bits (the decoder's order): there the bit
+    # count is unchanged, and so is the multiset of the other bytes
     allref = np.concatenate([np.ascontiguousarray(a).view(np.uint8).ravel()
                              for a in (codes, scales, biases) if a is not None])
-    assert np.array_equal(np.sort(allref), np.sort(t))
+    if fmt != "q3k":
+        assert np.array_equal(np.sort(allref), np.sort(t))
+    else:
+        blk = allref.reshape(-1, 110)
+        plane = rows * cols // 4  # the tiled code plane, then the hmask plane
+        hm = t[plane:plane + rows * (cols // 256) * 32]
+        assert np.unpackbits(hm).sum() == np.unpackbits(blk[:, :32]).sum()
+        rest = np.concatenate([t[:plane], t[plane + hm.size:]])
+        assert np.array_equal(np.sort(blk[:, 32:].ravel()), np.sort(rest))
+
+
+def test_q3k_tiled_hmask_bit_order(rng):
+    """Tiled Q3_K hmask word: ggml bit 4h + jj of byte k (half h, level jj)
+    at bit (2jj + 2 + (k & 1) + 16 (k >> 1) + 8h) mod 32, so that the decoder
+    finds the high bit of level jj of bytes 0 and 2 at bits 2jj + 2 and
+    2jj + 18 (bytes 1, 3 one higher; h = 1 rotated by 8).  One hand-placed
+    bit per (k, h, jj) through a one-block matrix."""
+    rows, cols = 16, 256
+    d = make_weights("q3k", rows, cols, rng)
+    codes = d["codes"].copy()
+    plane = rows * cols // 4
+    for k in range(4):
+        for h in range(2):
+            for jj in range(4):
+                blk = codes.view(np.uint8).reshape(rows, 110)
+                blk[:, :32] = 0
+                blk[0, 4 + k] = 1 << (4 * h + jj)  # hmask word 1 (j = 1), byte k
+                t = tq.repack_host(FMTS["q3k"], rows, cols, codes)
+                # row 0, block 0, plane entry j = 1, first word of the pair
+                off = plane + ((0 * 1 + 0) * 4 + 1) * 16 * 8
+                w = int(np.frombuffer(t[off:off + 4].tobytes(), np.uint32)[0])
+                assert w == 1 << ((2 * jj + 2 + (k & 1) + 16 * (k >> 1) + 8 * h) % 32), (k, h, jj)
 
 
 def test_repack_code_plane_is_lane_major(rng):

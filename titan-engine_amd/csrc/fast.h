@@ -897,19 +897,20 @@ struct FxQ3K {
             }
         return o;
     }
+    // the hmask bits of word step i in the tiled order (see tiled_q3k_hmask_off):
+    // half h = i >> 1 rotated down to the h = 0 positions
+    TQ_DEV static uint32_t hbits(const Raw& r, int i) {
+        const uint32_t p = (i & 1) ? r.hm1 : r.hm0;
+        return (i >> 1) ? __builtin_amdgcn_alignbit(p, p, 8) : p;
+    }
     // 3-bit code u = q2 + 4 * hbit of the 4 bytes of word step i at level jj
+    // (bytes 0, 2: hmask bit 2jj + 2 (+16) -> bit 2; bytes 1, 3: 2jj + 3 (+16))
     TQ_DEV static uint32_t code3(const Raw& r, int i, int jj) {
-        const uint32_t hm = (i & 1) ? r.hm1 : r.hm0;
-        return ((r.w[i] >> (2 * jj)) & 0x03030303u) | (((hm >> (4 * (i >> 1) + jj)) & 0x01010101u) << 2);
+        const uint32_t x = hbits(r, i);
+        return ((r.w[i] >> (2 * jj)) & 0x03030303u) | ((x >> (2 * jj)) & 0x00040004u) |
+               ((x << (7 - 2 * jj)) & 0x04000400u);
     }
-    // the same codes in bits 0..2 of each byte, bits 3..7 undefined: two
-    // shifts and one bit-field insert
-    TQ_DEV static uint32_t code3x(const Raw& r, int i, int jj) {
-        const uint32_t hm = (i & 1) ? r.hm1 : r.hm0;
-        const int sh = 4 * (i >> 1) + jj - 2;  // hmask bit -> bit 2 of the byte
-        const uint32_t y = sh >= 0 ? hm >> sh : hm << -sh;
-        return ((r.w[i] >> (2 * jj)) & 0x03030303u) | (y & ~0x03030303u);
-    }
+    TQ_DEV static uint32_t code3x(const Raw& r, int i, int jj) { return code3(r, i, jj); }
     TQ_DEV static float bias(const Dec& d, const float* s16) {
         // value = d*sc*(u - 4): the -4 term is -4 d sc sum(x) per sub-block
         float t = 0.0f;
@@ -960,13 +961,14 @@ struct FxQ3K {
     // SX: the codes u of level jj in place as fp16 subnormals, u * 2^(2jj-24):
     // bits 2jj, 2jj+1 of the byte from the 2-bit word, bit 2jj+2 from the
     // hmask; the halves hold bytes (0, 2) and (1, 3) of the word
+    // (the tiled hmask order puts the high bit of level jj of bytes 0, 2 at
+    // bit 2jj + 2 of the word and of bytes 1, 3 one bit higher: no shift per
+    // level)
     TQ_DEV static h4_t codes_in_place(const Raw& r, int i, int jj) {
         const uint32_t w = r.w[i], w8 = w >> 8;
-        const uint32_t hm = (i & 1) ? r.hm1 : r.hm0, hm8 = hm >> 8;
-        const int sh = 4 * (i >> 1) + jj - (2 * jj + 2);  // hmask bit -> bit 2jj+2
-        const uint32_t hb = sh >= 0 ? hm >> sh : hm << -sh, hb8 = sh >= 0 ? hm8 >> sh : hm8 << -sh;
+        const uint32_t x = hbits(r, i), x1 = x >> 1;
         const uint32_t mq = 0x00030003u << (2 * jj), mh = 0x00040004u << (2 * jj);
-        return h4_of((w & mq) | (hb & mh), (w8 & mq) | (hb8 & mh));
+        return h4_of((w & mq) | (x & mh), (w8 & mq) | (x1 & mh));
     }
     template <int NB, int GS, bool SX>
     TQ_DEV static void issue(const Raw& r, int j, const _Float16* const* xt, Tmp<NB, GS, SX>& T) {

@@ -126,8 +126,10 @@ TQ_DEV float elem(const WDesc& w, int row, int col) {
             dh = blk[108] | (blk[109] << 8);
         } else {
             qb = w.codes[tiled_code_byte(g, row, b * 64 + 32 * h + l)];
-            // hmask byte l: word l/4 = 4*hi + j  ->  plane entry j, half hi
-            hb = w.codes[tiled_q3k_hmask_off(g, row, b, (l >> 2) & 3) + 4 * (l >> 4) + (l & 3)];
+            // hmask byte l: word l/4 = 4*hi + j  ->  plane entry j, half hi; its
+            // bit 4h + jj at q3k_hpos(l % 4, jj, h) of the tiled word
+            const uint32_t hw = ld_u32(w.codes + tiled_q3k_hmask_off(g, row, b, (l >> 2) & 3) + 4 * (l >> 4));
+            hb = ((hw >> q3k_hpos(l & 3, jj, h)) & 1u) << (4 * h + jj);
             const uint8_t* sp = w.codes + tiled_q3k_sc_off(g, row, b);
             s0 = ld_u32(sp);
             s1 = ld_u32(sp + 4);

@@ -119,7 +119,28 @@ TQ_HD size_t tiled_q4k_hdr_off(const Geo& g, int row, int blk) {
            (((size_t)(row >> 4) * g.nblk + blk) * 16 + (row & 15)) * 16;
 }
 // Q3_K: hmask words (j, 4+j) (8 B) at [t][blk][j][r]; scales (12 B) at
-// [t][blk][r]; d (2 B) at [t][blk][r].
+// [t][blk][r]; d (2 B) at [t][blk][r].  Each tiled hmask word holds the 32
+// bits of one ggml hmask word (bytes k = 0..3 of four positions, bit 4h + jj
+// of byte k: half h, level jj) re-ordered for the decoder: bit (h, jj, k) at
+// q3k_hpos(k, jj, h).  For h = 0, bytes 0 and 2 of level jj sit at bits
+// 2jj + 2 and 2jj + 18 -- where the 3-bit code of level jj needs its high
+// bit inside the fp16 halves of bytes (0, 2) -- and bytes 1, 3 one bit
+// higher; h = 1 is the same pattern rotated by 8 bits.
+TQ_HD int q3k_hpos(int k, int jj, int h) { return (2 * jj + 2 + (k & 1) + 16 * (k >> 1) + 8 * h) & 31; }
+TQ_HD uint32_t q3k_hm_pack(uint32_t w) {
+    uint32_t o = 0;
+    for (int k = 0; k < 4; k++)
+        for (int h = 0; h < 2; h++)
+            for (int jj = 0; jj < 4; jj++) o |= ((w >> (8 * k + 4 * h + jj)) & 1u) << q3k_hpos(k, jj, h);
+    return o;
+}
+TQ_HD uint32_t q3k_hm_unpack(uint32_t p) {
+    uint32_t w = 0;
+    for (int k = 0; k < 4; k++)
+        for (int h = 0; h < 2; h++)
+            for (int jj = 0; jj < 4; jj++) w |= ((p >> q3k_hpos(k, jj, h)) & 1u) << (8 * k + 4 * h + jj);
+    return w;
+}
 TQ_HD size_t tiled_q3k_hmask_off(const Geo& g, int row, int blk, int j) {
     return tiled_code_plane_bytes(g) +
            ((((size_t)(row >> 4) * g.nblk + blk) * 4 + j) * 16 + (row & 15)) * 8;

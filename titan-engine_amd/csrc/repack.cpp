@@ -97,10 +97,13 @@ extern "C" int titan_repack_host(int fmt, int rows, int cols, int gs, const void
             case TITAN_Q3_K:
                 for (int b = 0; b < g.nblk; b++) {
                     const uint8_t* blk = blocks + ((size_t)r * g.nblk + b) * 110;
-                    for (int j = 0; j < 4; j++) {
-                        memcpy(out + tq::tiled_q3k_hmask_off(g, r, b, j), blk + 4 * j, 4);
-                        memcpy(out + tq::tiled_q3k_hmask_off(g, r, b, j) + 4, blk + 16 + 4 * j, 4);
-                    }
+                    for (int j = 0; j < 4; j++)
+                        for (int hi = 0; hi < 2; hi++) {  // hmask words j, 4 + j
+                            uint32_t w;
+                            memcpy(&w, blk + 16 * hi + 4 * j, 4);
+                            w = tq::q3k_hm_pack(w);
+                            memcpy(out + tq::tiled_q3k_hmask_off(g, r, b, j) + 4 * hi, &w, 4);
+                        }
                     memcpy(out + tq::tiled_q3k_sc_off(g, r, b), blk + 96, 12);
                     memcpy(out + tq::tiled_q3k_d_off(g, r, b), blk + 108, 2);
                 }
@@ -166,10 +169,13 @@ extern "C" int titan_unpack_host(int fmt, int rows, int cols, int gs, const void
             case TITAN_Q3_K:
                 for (int b = 0; b < g.nblk; b++) {
                     uint8_t* blk = c8 + ((size_t)r * g.nblk + b) * 110;
-                    for (int j = 0; j < 4; j++) {
-                        memcpy(blk + 4 * j, in + tq::tiled_q3k_hmask_off(g, r, b, j), 4);
-                        memcpy(blk + 16 + 4 * j, in + tq::tiled_q3k_hmask_off(g, r, b, j) + 4, 4);
-                    }
+                    for (int j = 0; j < 4; j++)
+                        for (int hi = 0; hi < 2; hi++) {
+                            uint32_t w;
+                            memcpy(&w, in + tq::tiled_q3k_hmask_off(g, r, b, j) + 4 * hi, 4);
+                            w = tq::q3k_hm_unpack(w);
+                            memcpy(blk + 16 * hi + 4 * j, &w, 4);
+                        }
                     memcpy(blk + 96, in + tq::tiled_q3k_sc_off(g, r, b), 12);
                     memcpy(blk + 108, in + tq::tiled_q3k_d_off(g, r, b), 2);
                 }
