@@ -72,7 +72,9 @@ enum {
  *                      buffer of planes, 16-row tiles, each 64-byte column
  *                      chunk of 16 rows stored as 1 KiB in wave-lane order so
  *                      that one wave's 64 x 16-byte loads are contiguous.  A
- *                      byte permutation of the REF bytes (same size). */
+ *                      byte permutation of the REF bytes (same size), except
+ *                      that Q3_K's hmask words also have their bits re-ordered
+ *                      for the decoder; titan_unpack_host inverts it exactly. */
 enum { TITAN_LAYOUT_REF = 0, TITAN_LAYOUT_TILED = 1 };
 
 /* A quantized weight matrix W [rows][cols] (rows = output features). */
