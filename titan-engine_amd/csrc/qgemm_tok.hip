@@ -1,4 +1,4 @@
-// qgemm_tok.hip -- INT4 dequant-GEMM for several tokens (M >= 9), TILED layout.
+// qgemm_tok.hip -- INT4 dequant-GEMM for several tokens (M >= 5), TILED layout.
 //
 // Y[m][r] = sum_c x[m][c] * (q[r][c] * s[r][g] + b[r][g]),  g = c / group_size
 // (dequant.cu:23-104 semantics, fp32 accumulation) for up to TITAN_MAX_BATCH
