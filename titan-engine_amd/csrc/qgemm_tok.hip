@@ -21,6 +21,7 @@
 // sums come from one more MFMA against ones, shared by the RT tiles.
 #include "common.h"
 #include "layout.h"
+#include "fast.h"
 #include "qgemm_tok.h"
 #include "xitem.h"
 
@@ -66,7 +67,12 @@ TQ_DEV th8 tok_b8(uint32_t w) {
 // columns each) per scale fold.
 // STREAM: one token tile reads each weight once (nontemporal loads); with
 // more tiles the later tiles re-read the codes from the caches.
-template <int TM, int RT, int FW, int XDT, int ODT, bool STREAM>
+// BF (launches of up to 8 tokens): every load issued without a branch and the
+// activations two slabs ahead (three register sets, like the weights); the
+// slab count is rounded up to whole triples, the extra slabs reading zero
+// codes and their folds discarded.  8B layer: 5 tokens 31.8 -> 28.2 us,
+// 8 tokens 32.4 -> 30.4 us; from 12 tokens on it measured 2-6% slower.
+template <int TM, int RT, int FW, int XDT, int ODT, bool STREAM, bool BF>
 __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) {
     constexpr int NB = TM / 16;
     constexpr int NI = TM * kTokSlab / 8 / 64;  // staging items per lane
@@ -95,14 +101,22 @@ __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) 
     const int gshift = 31 - __builtin_clz(P.gs);  // group = column >> gshift
     _Float16* xs = xs_all + wave * XS;
 
-    // tile q (clamped past the last row: loaded, never stored)
+    // tile q (clamped past the last row: loaded, never stored).  BF: its
+    // codes through a buffer resource over this wave's slabs (a slab past
+    // the wave's last one reads zeros and fetches nothing), the activation
+    // and scale slabs clamped into [0, s_end).
     uint32_t code_off[RT], sb_base[RT];
+    CodeSrc csrc[RT];
+    const uint32_t lane16 = (uint32_t)(j * 16 + r) * 16u;
 #pragma unroll
     for (int q = 0; q < RT; q++) {
         const int t = min((rb0 >> 4) + q, ntile - 1);
         code_off[q] = (uint32_t)tiled_code_off(geo, t * 16 + r, 0, j);
         sb_base[q] = (uint32_t)tiled_sb_off(geo, t * 16 + r, 0);
+        csrc[q] = CodeSrc{P.w + ((size_t)t * geo.nchunks + s_beg) * 1024u,
+                          (uint32_t)(s_end > s_beg ? s_end - s_beg : 0) * 1024u, lane16};
     }
+    auto in_k = [&](int s) { return BF ? max(min(s, s_end - 1), 0) : s; };
 
     // staging: item it covers token row rr, columns [8 cg, 8 cg + 8) of a slab
     int64_t src[NI];
@@ -114,23 +128,29 @@ __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) 
         src[it] = rr < nt ? (int64_t)(t0 + rr) * P.ldx + cg * 8 : -1;
     }
     auto load_x = [&](int s, XItem<XDT>* xr) {
+        const int sk = in_k(s);
 #pragma unroll
         for (int it = 0; it < NI; it++) {
-            if (src[it] >= 0) xr[it].load(P.x, src[it] + (int64_t)s * kTokSlab);
+            if (src[it] >= 0) xr[it].load(P.x, src[it] + (int64_t)sk * kTokSlab);
             else xr[it].zero();
         }
     };
     struct WSet { uint4 c[RT]; uint32_t sb[RT][NF]; };
     auto load_w = [&](int s, WSet& w) {
+        const int sk = in_k(s);
 #pragma unroll
         for (int q = 0; q < RT; q++) {
-            const uint8_t* cp = P.w + code_off[q] + (uint32_t)s * 1024u;
-            w.c[q] = STREAM ? ld_stream_u128(cp) : *(const uint4*)cp;
+            if constexpr (BF) {
+                w.c[q] = ld_code_chunk<STREAM>(csrc[q].at(s - s_beg), lane16, 0);
+            } else {
+                const uint8_t* cp = P.w + code_off[q] + (uint32_t)s * 1024u;
+                w.c[q] = STREAM ? ld_stream_u128(cp) : *(const uint4*)cp;
+            }
 #pragma unroll
             for (int f = 0; f < NF; f++) {
                 // scale slot: one per chunk for groups of a chunk or more, else one per group
-                const uint32_t g = (uint32_t)((s * kTokSlab + f * FW * 32) >> gshift);
-                const uint32_t sl = P.gs >= kTokSlab ? (uint32_t)s : g;
+                const uint32_t g = (uint32_t)((sk * kTokSlab + f * FW * 32) >> gshift);
+                const uint32_t sl = P.gs >= kTokSlab ? (uint32_t)sk : g;
                 w.sb[q][f] = *(const uint32_t*)(P.w + sb_base[q] + (sl >> 2) * 256u + (sl & 3u) * 4u);
             }
         }
@@ -147,18 +167,29 @@ __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) 
     // rotating register sets.  The stage is the wave's own, and LDS
     // operations of one wave complete in order, so a slab's reads finish
     // before the next slab overwrites it.
-    XItem<XDT> xr[NI];
+    XItem<XDT> x0[NI], x1[NI], x2[NI];  // x1, x2: BF only
     WSet w0, w1, w2;
-    if (s_beg < s_end) {
-        load_x(s_beg, xr);
+    if constexpr (BF) {
+        load_x(s_beg, x0);
+        load_w(s_beg, w0);
+        load_x(s_beg + 1, x1);
+        load_w(s_beg + 1, w1);
+    } else if (s_beg < s_end) {
+        load_x(s_beg, x0);
         load_w(s_beg, w0);
         if (s_beg + 1 < s_end) load_w(s_beg + 1, w1);
     }
-    auto step = [&](int s, const WSet& wc, WSet& wnext2) {
+    auto step = [&](int s, const WSet& wc, WSet& wnext2, XItem<XDT>* xc, XItem<XDT>* xnext2) {
+        const bool live = !BF || s < s_end;
 #pragma unroll
-        for (int it = 0; it < NI; it++) *(uint4*)(xs + ldsi[it]) = tok_perm8(xr[it].h());
-        if (s + 1 < s_end) load_x(s + 1, xr);
-        if (s + 2 < s_end) load_w(s + 2, wnext2);
+        for (int it = 0; it < NI; it++) *(uint4*)(xs + ldsi[it]) = tok_perm8(xc[it].h());
+        if constexpr (BF) {
+            load_x(s + 2, xnext2);
+            load_w(s + 2, wnext2);
+        } else {
+            if (s + 1 < s_end) load_x(s + 1, xc);
+            if (s + 2 < s_end) load_w(s + 2, wnext2);
+        }
 #pragma unroll
         for (int f = 0; f < NF; f++) {
             tf4 C[RT][NB], O[NB];
@@ -192,17 +223,25 @@ __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) 
                 for (int b = 0; b < NB; b++) {
                     if (b < nb) {
 #pragma unroll
-                        for (int v = 0; v < 4; v++)
-                            acc[q][b][v] = __builtin_fmaf(bi, O[b][v], __builtin_fmaf(sc, C[q][b][v], acc[q][b][v]));
+                        for (int v = 0; v < 4; v++) {
+                            const float nv = __builtin_fmaf(bi, O[b][v], __builtin_fmaf(sc, C[q][b][v], acc[q][b][v]));
+                            acc[q][b][v] = live ? nv : acc[q][b][v];
+                        }
                     }
                 }
             }
         }
     };
     for (int s = s_beg; s < s_end; s += 3) {
-        step(s, w0, w2);
-        if (s + 1 < s_end) step(s + 1, w1, w0);
-        if (s + 2 < s_end) step(s + 2, w2, w1);
+        if constexpr (BF) {
+            step(s, w0, w2, x0, x2);
+            step(s + 1, w1, w0, x1, x0);
+            step(s + 2, w2, w1, x2, x1);
+        } else {
+            step(s, w0, w2, x0, x0);
+            if (s + 1 < s_end) step(s + 1, w1, w0, x0, x0);
+            if (s + 2 < s_end) step(s + 2, w2, w1, x0, x0);
+        }
     }
 
     // reduce the 4 K quarters: wave w sums tiles q = w, w + 4, ... in wave order
@@ -241,10 +280,12 @@ template <int TM, int RT, int FW, int XDT, int ODT>
 void launch_tok(const TokArgs& a, int maxrows, hipStream_t st) {
     const int nrb = ((maxrows + 16 * RT - 1) / (16 * RT) + 7) / 8 * 8;
     dim3 grid(nrb * ((a.M + TM - 1) / TM), TITAN_MAX_BATCH, 1);
-    if (a.M <= TM)
-        hipLaunchKernelGGL((qgemm_tok_int4_kernel<TM, RT, FW, XDT, ODT, true>), grid, dim3(kTokThreads), 0, st, a);
+    if (TM == 16 && a.M <= 8)
+        hipLaunchKernelGGL((qgemm_tok_int4_kernel<TM, RT, FW, XDT, ODT, true, true>), grid, dim3(kTokThreads), 0, st, a);
+    else if (a.M <= TM)
+        hipLaunchKernelGGL((qgemm_tok_int4_kernel<TM, RT, FW, XDT, ODT, true, false>), grid, dim3(kTokThreads), 0, st, a);
     else
-        hipLaunchKernelGGL((qgemm_tok_int4_kernel<TM, RT, FW, XDT, ODT, false>), grid, dim3(kTokThreads), 0, st, a);
+        hipLaunchKernelGGL((qgemm_tok_int4_kernel<TM, RT, FW, XDT, ODT, false, false>), grid, dim3(kTokThreads), 0, st, a);
 }
 
 template <int TM, int RT, int FW, int XDT>
