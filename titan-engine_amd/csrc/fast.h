@@ -671,7 +671,12 @@ struct FxQ4K {
     static constexpr long long WAVES_TARGET_M1 = 1536;
     struct Off { uint32_t c, h; };
     struct Raw { uint32_t w[4]; uint4 hdr; };
-    struct Dec { float ds[4], dm[4]; };  // [2*c4' + (0: low / 1: high)]
+    // decode<GS>(w, raw, c, j) uses only the parity of c (which half block)
+    static constexpr bool HALF_FROM_U = true;
+    // [2*c4' + (0: low / 1: high nibbles)]: ds = d sc 2^24 (low) or
+    // d sc 2^20 (high, whose codes sit x16), the MFMA fold's code scales;
+    // dm = -dmin m
+    struct Dec { float ds[4], dm[4]; };
     TQ_DEV static Off base(const WDesc& w, int row, int j) {
         const Geo& g = w.g;
         if constexpr (LAYOUT == TITAN_LAYOUT_REF)
@@ -710,17 +715,18 @@ struct FxQ4K {
         const uint32_t SC = (a_sc & 0x0F0F0F0Fu) | ((b_sc >> 2) & 0x30303030u);
         const uint32_t MN = (a_m & 0x0F0F0F0Fu) | ((b_m >> 2) & 0x30303030u);
         Dec o;
+        const float dlo = d * kTwo24, dhi = d * (kTwo24 / 16.0f), nmin = -dmin;  // exact scalings
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            o.ds[k] = d * (float)((SC >> (8 * k)) & 0xFFu);
-            o.dm[k] = dmin * (float)((MN >> (8 * k)) & 0xFFu);
+            o.ds[k] = (k & 1 ? dhi : dlo) * (float)((SC >> (8 * k)) & 0xFFu);
+            o.dm[k] = nmin * (float)((MN >> (8 * k)) & 0xFFu);
         }
         return o;
     }
     TQ_DEV static float bias(const Dec& d, const float* s16) {
         float t = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) t = __builtin_fmaf(-d.dm[k], s16[2 * k] + s16[2 * k + 1], t);
+        for (int k = 0; k < 4; k++) t = __builtin_fmaf(d.dm[k], s16[2 * k] + s16[2 * k + 1], t);
         return t;
     }
     TQ_DEV static float fold_f32(const Raw& r, const Dec& d, int j, const float* xc, const float* s16) {
@@ -740,8 +746,8 @@ struct FxQ4K {
             b = __builtin_fmaf((float)((hi >> 8) & 0xFF), xb[1], b);
             b = __builtin_fmaf((float)((hi >> 16) & 0xFF), xb[2], b);
             b = __builtin_fmaf((float)(hi >> 24), xb[3], b);
-            t = __builtin_fmaf(d.ds[2 * (i >> 1)], a, t);
-            t = __builtin_fmaf(d.ds[2 * (i >> 1) + 1], b, t);
+            t = __builtin_fmaf(d.ds[2 * (i >> 1)] * (1.0f / kTwo24), a, t);  // d sc (exact)
+            t = __builtin_fmaf(d.ds[2 * (i >> 1) + 1] * (16.0f / kTwo24), b, t);
         }
         return j == 0 ? t + bias(d, s16) : t;
     }
@@ -755,8 +761,8 @@ struct FxQ4K {
             a = dot2(u & 0x000F000Fu, xv.y, a);           // bytes (1, 3)
             float b = dot2(w & 0x00F000F0u, xv.z, 0.0f);  // high nibbles x16
             b = dot2(u & 0x00F000F0u, xv.w, b);
-            t = __builtin_fmaf(d.ds[2 * (i >> 1)], a * kTwo24, t);
-            t = __builtin_fmaf(d.ds[2 * (i >> 1) + 1], b * (kTwo24 / 16.0f), t);
+            t = __builtin_fmaf(d.ds[2 * (i >> 1)], a, t);
+            t = __builtin_fmaf(d.ds[2 * (i >> 1) + 1], b, t);
         }
         return j == 0 ? t + bias(d, s16) : t;
     }
@@ -791,8 +797,8 @@ struct FxQ4K {
     TQ_DEV static void finish(const Tmp<NB, GS, SX>& T, const Dec& d, const float* sx, f4_t* acc) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const float sa = d.ds[2 * h] * kTwo24, sb = d.ds[2 * h + 1] * (kTwo24 / 16.0f);
-            const float ma = -d.dm[2 * h], mb = -d.dm[2 * h + 1];
+            const float sa = d.ds[2 * h], sb = d.ds[2 * h + 1];
+            const float ma = d.dm[2 * h], mb = d.dm[2 * h + 1];
             float4 xa, xb;  // sub-block sums (32 columns each) for tokens 0..3
             if constexpr (SX) {
                 xa = *(const float4*)(sx + 4 * (2 * h));

@@ -270,6 +270,17 @@ TQ_DEV void stage_f16(_Float16* xh, float* s16, int pc, const void* x, int64_t l
 template <class F, int M, int MODE>
 constexpr int gemv_u() { return TQ_GEMV_U; }
 
+template <class F, class = void>
+struct has_half_from_u : std::false_type {};
+template <class F>
+struct has_half_from_u<F, std::void_t<decltype(F::HALF_FROM_U)>> : std::true_type {};
+template <class F>
+constexpr bool half_from_u() {
+    if constexpr (has_half_from_u<F>::value) return F::HALF_FROM_U;
+    else return false;
+}
+static_assert(TQ_GEMV_U % 2 == 0, "chunk groups start at even chunks");
+
 // Formats whose tiled scales come in 16-byte cells (SB_CELL) decode chunk u
 // of a group from the cell loaded with chunk u - u % GS.
 template <class F>
@@ -280,6 +291,10 @@ constexpr bool has_sb_cell() {
 template <class F, int GS, class RawArr>
 TQ_DEV typename F::Dec decode_u(const WDesc& W, const RawArr& R, int u, int cc, int j) {
     if constexpr (has_sb_cell<F>()) return F::template decode_cell<GS>(R[u - u % GS].q, u);
+    // HALF_FROM_U: the decoder needs only the chunk's parity, and chunk
+    // groups start at a multiple of U (even), so u's parity is the chunk's:
+    // known at compile time
+    else if constexpr (half_from_u<F>()) return F::template decode<GS>(W, R[u], u, j);
     else return F::template decode<GS>(W, R[u], cc, j);
 }
 
