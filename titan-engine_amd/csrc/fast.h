@@ -770,25 +770,26 @@ struct FxQ4K {
     struct Tmp { f4_t CA[2][NB], CB[2][NB], OA[SX ? 1 : 2][NB], OB[SX ? 1 : 2][NB]; };
     template <int NB, int GS, bool SX>
     TQ_DEV static void issue(const Raw& r, int j, const _Float16* const* xt, Tmp<NB, GS, SX>& T) {
-        const h4_t ones = h4_of(kOnes2, kOnes2);
+        // word steps i = 2h and 2h + 1 fold into the same sub-block tiles: one
+        // 16x16x32 step over both (A and B take their columns in the same
+        // order, so the products pair up as in two 16x16x16 steps)
+        const h8_t ones = h8_of(make_uint4(kOnes2, kOnes2, kOnes2, kOnes2));
 #pragma unroll
         for (int h = 0; h < 2; h++) {  // the two 64-element groups of the chunk
+            const uint32_t w0 = r.w[2 * h], u0 = w0 >> 8, w1 = r.w[2 * h + 1], u1 = w1 >> 8;
+            const h8_t blo = h8_of(make_uint4(w0 & 0x000F000Fu, u0 & 0x000F000Fu, w1 & 0x000F000Fu, u1 & 0x000F000Fu));
+            const h8_t bhi = h8_of(make_uint4(w0 & 0x00F000F0u, u0 & 0x00F000F0u, w1 & 0x00F000F0u,
+                                              u1 & 0x00F000F0u));  // x16
 #pragma unroll
-            for (int ii = 0; ii < 2; ii++) {
-                const int i = 2 * h + ii;
-                const uint32_t w = r.w[i], u = w >> 8;
-                const h4_t blo = h4_of(w & 0x000F000Fu, u & 0x000F000Fu);
-                const h4_t bhi = h4_of(w & 0x00F000F0u, u & 0x00F000F0u);  // x16
-#pragma unroll
-                for (int n = 0; n < NB; n++) {
-                    const uint4 xv = *(const uint4*)(xt[n] + 64 * h + 8 * (4 * ii + j));
-                    const h4_t xa = h4_of(xv.x, xv.y), xb = h4_of(xv.z, xv.w);
-                    T.CA[h][n] = mfma16(xa, blo, ii == 0 ? f4_zero() : T.CA[h][n]);
-                    T.CB[h][n] = mfma16(xb, bhi, ii == 0 ? f4_zero() : T.CB[h][n]);
-                    if constexpr (!SX) {
-                        T.OA[h][n] = mfma16(xa, ones, ii == 0 ? f4_zero() : T.OA[h][n]);
-                        T.OB[h][n] = mfma16(xb, ones, ii == 0 ? f4_zero() : T.OB[h][n]);
-                    }
+            for (int n = 0; n < NB; n++) {
+                const uint4 x0 = *(const uint4*)(xt[n] + 64 * h + 8 * j);
+                const uint4 x1 = *(const uint4*)(xt[n] + 64 * h + 8 * (4 + j));
+                const h8_t xa = h8_of(make_uint4(x0.x, x0.y, x1.x, x1.y)), xb = h8_of(make_uint4(x0.z, x0.w, x1.z, x1.w));
+                T.CA[h][n] = mfma32(xa, blo, f4_zero());
+                T.CB[h][n] = mfma32(xb, bhi, f4_zero());
+                if constexpr (!SX) {
+                    T.OA[h][n] = mfma32(xa, ones, f4_zero());
+                    T.OB[h][n] = mfma32(xb, ones, f4_zero());
                 }
             }
         }
