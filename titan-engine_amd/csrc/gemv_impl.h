@@ -357,10 +357,16 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_kernel(GemvArgs a) {
     // this workgroup's problem: a count over the first-workgroup table, with
     // no chain of dependent scalar loads (a scan over the problems one by one
     // took 2 us to issue the first load of a seven-problem launch)
-    const int bid = blockIdx.x;
+    // One-problem launches come as a (1, workgroups) grid: their workgroups
+    // have blockIdx.x == 0 and skip the table, so the problem's own scalar
+    // loads are the first ones (one round trip less before the first
+    // weight load); other launches are (workgroups, 1).
+    const int bid = blockIdx.x + blockIdx.y;
     int pi = 0;
+    if (blockIdx.x != 0) {
 #pragma unroll
-    for (int i = 1; i < kGemvMaxProbs; i++) pi += bid >= a.wgb[i] ? 1 : 0;
+        for (int i = 1; i < kGemvMaxProbs; i++) pi += bid >= a.wgb[i] ? 1 : 0;
+    }
     const GemvProb& P = a.p[pi];
     const WDesc& W = P.w;
     const int rows = W.g.rows;
@@ -1096,7 +1102,8 @@ void launch_mode(const GemvArgs& args, int, hipStream_t st) {
         }
         auto go = [&](auto kern) {
             if (lds > 64 * 1024) set_max_lds((const void*)kern);
-            hipLaunchKernelGGL(kern, dim3(wg), dim3(kGemvThreads), lds, st, b);
+            const dim3 grid = b.n == 1 ? dim3(1, wg) : dim3(wg, 1);
+            hipLaunchKernelGGL(kern, grid, dim3(kGemvThreads), lds, st, b);
         };
         if constexpr (allow_exact<F>()) {
             if (exact) {
@@ -1115,7 +1122,8 @@ void launch_mode(const GemvArgs& args, int, hipStream_t st) {
         constexpr bool grouped = F::FMT == TITAN_INT4 || F::FMT == TITAN_INT2 || F::FMT == TITAN_FP4;
         auto go = [&](auto kern) {
             if (lds > 64 * 1024) set_max_lds((const void*)kern);
-            hipLaunchKernelGGL(kern, dim3(wg), dim3(kGemvThreads), lds, st, b);
+            const dim3 grid = b.n == 1 ? dim3(1, wg) : dim3(wg, 1);
+            hipLaunchKernelGGL(kern, grid, dim3(kGemvThreads), lds, st, b);
         };
         if (grouped && gsteps == 1) go(qgemv_kernel<F, M, MODE, 1>);
         else if (grouped && gsteps == 2) go(qgemv_kernel<F, M, MODE, 2>);
