@@ -8,13 +8,10 @@
 // ============================================================================
 namespace {
 
-#ifndef TQ_TOK_MIN
-#define TQ_TOK_MIN 5
-#endif
 // token count from which INT4 tiled weights go to the token-tiled kernel
 // (8B layer: 5-8 tokens 32 us there against 33-34 us in the GEMV; 4 tokens
 // 26.6 us in the GEMV)
-constexpr int kTokMinTokens = TQ_TOK_MIN;
+constexpr int kTokMinTokens = 5;
 
 using namespace tq;
 

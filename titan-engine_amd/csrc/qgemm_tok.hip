@@ -365,23 +365,13 @@ int run_tok_int4(const titan_qweight* Ws, const void* const* Xs, const int64_t* 
     }
     const int gs = Ws[0].group_size;
     const int fw = gs >= 128 ? 4 : gs / 32;
-    // token tile: the fewest 16-token blocks that cover M in one tile, up to 64
-#ifndef TQ_TOK_T16
-#define TQ_TOK_T16 64     // largest M served by 16-token tiles (one tile per 16 tokens)
-#endif
-#ifndef TQ_TOK_RTA
-#define TQ_TOK_RTA 2
-#endif
-#ifndef TQ_TOK_RTB
-#define TQ_TOK_RTB 4
-#endif
-#ifndef TQ_TOK_RT32
-#define TQ_TOK_RT32 2
-#endif
-    // one 16-token tile: two row tiles per wave; several token tiles: four
-    if (M <= 16) tq::launch_tok_f<16, TQ_TOK_RTA>(a, maxrows, fw, xdt, ydt, st);
-    else if (M <= TQ_TOK_T16) tq::launch_tok_f<16, TQ_TOK_RTB>(a, maxrows, fw, xdt, ydt, st);
-    else if (M <= 32) tq::launch_tok_f<32, TQ_TOK_RT32>(a, maxrows, fw, xdt, ydt, st);
+    // token tile and row tiles per wave (measured on the 8B layer): one
+    // 16-token tile with two row tiles up to 16 tokens; 16-token tiles with
+    // four row tiles up to 64 tokens (32-token tiles, or two row tiles,
+    // measured 1-8% slower at 24 and 32 tokens); 64-token tiles beyond
+    constexpr int kT16Max = 64;  // largest M served by 16-token tiles
+    if (M <= 16) tq::launch_tok_f<16, 2>(a, maxrows, fw, xdt, ydt, st);
+    else if (M <= kT16Max) tq::launch_tok_f<16, 4>(a, maxrows, fw, xdt, ydt, st);
     else tq::launch_tok_f<64, 2>(a, maxrows, fw, xdt, ydt, st);
     return launch_status();
 }
