@@ -200,8 +200,9 @@ def test_batched_launch_matches_single(lay, rng):
 @pytest.mark.parametrize("rows,cols,gs", [(64, 512, 128), (80, 384, 32), (208, 1024, 64),
                                           (128, 768, 256)])
 def test_int4_token_tiled_parity(M, rows, cols, gs, rng):
-    """INT4 tiled with M >= 9 runs the token-tiled dequant-GEMM (M = 8 the GEMV; partial row
-    blocks, every group size class, token tiles of 16/32/64 and several tiles)."""
+    """INT4 tiled with M >= 5 runs the token-tiled dequant-GEMM (up to 8 tokens its
+    branch-free loop; partial row blocks, every group size class, one and several 16-token
+    tiles, 64-token tiles)."""
     d = make_weights("int4", rows, cols, rng, gs=gs)
     W = upload(d, tq.LAYOUT_TILED)
     for xdt, ydt in [("f16", "f16"), ("bf16", "f32"), ("f32", "bf16")]:
