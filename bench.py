@@ -493,6 +493,8 @@ def main():
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--fp8-only", action="store_true",
                     help="only the two FP8 prefill GEMMs (for counter runs); prints their lines")
+    ap.add_argument("--int4-layer-tokens", type=int, default=0,
+                    help="only the INT4 8B layer at this token count (for counter runs); prints its line")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM byte-counter calibration)")
@@ -518,6 +520,13 @@ def main():
             lines.append(dict(config=f"FP8 E4M3 GEMM M={M} N={N} K={Kd}", ms=round(r["ms"], 4),
                               gemm_only_TFLOPS=round(r["gemm_tflops"], 1)))
         print(json.dumps(lines))
+        return
+
+    if args.int4_layer_tokens > 0:
+        M = args.int4_layer_tokens
+        r = bench_int4_layer(M, K, W, gen)
+        print(json.dumps(dict(config="INT4 g128 Llama-3-8B layer", M=M, ms=round(r["ms"], 4),
+                              GBps=round(r["gbs"], 1), frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4))))
         return
 
     log("headline: INT4 g128 Llama-3-8B layer, M=1")
