@@ -904,15 +904,18 @@ void launch_mode(const GemvArgs& args, int, hipStream_t st) {
     // 8.2 -> 10.2 us) the partials' round trips cost more than the extra
     // waves gain, so they keep the single-workgroup tiles.
     // The split aims for the same wave count as the in-workgroup split (the
-    // smaller of TQ_GEMV_XS_WAVES and the format's target): a launch that the
-    // format's target already considers full (Q3_K / INT2 28672 x 8192 at
-    // 1792 waves against a 1536 target) keeps its single-workgroup tiles.
+    // smaller of TQ_GEMV_XS_WAVES and the format's target) and engages only
+    // for launches of at most half that many waves: one the format already
+    // counts as full (Q3_K / INT2 28672 x 8192 at 1792 waves against a 1536
+    // target), or close to full, keeps its single-workgroup tiles and the
+    // tail split below (INT2 28672 x 8192, one token: split 20.4 us, tail
+    // split 18.4 us).
     if (a.ws && F::CHUNK_COLS > 128) {
         constexpr int U = gemv_u<F, M, MODE>();
         constexpr long long xs_waves = wt < TQ_GEMV_XS_WAVES ? wt : TQ_GEMV_XS_WAVES;
         long long waves = 0;
         for (int i = 0; i < a.n; i++) waves += (long long)a.p[i].ntiles << a.p[i].ks_log;
-        if (waves < xs_waves) {
+        if (2 * waves <= xs_waves) {
             int xs = 0;
             long long w0 = 0;
             for (int i = 0; i < a.n; i++) w0 += a.p[i].ntiles;
