@@ -908,8 +908,7 @@ void launch_mode(const GemvArgs& args, int, hipStream_t st) {
     // for launches of at most half that many waves: one the format already
     // counts as full (Q3_K / INT2 28672 x 8192 at 1792 waves against a 1536
     // target), or close to full, keeps its single-workgroup tiles and the
-    // tail split below (INT2 28672 x 8192, one token: split 20.4 us, tail
-    // split 18.4 us).
+    // tail split below, which needs no partials.
     if (a.ws && F::CHUNK_COLS > 128) {
         constexpr int U = gemv_u<F, M, MODE>();
         constexpr long long xs_waves = wt < TQ_GEMV_XS_WAVES ? wt : TQ_GEMV_XS_WAVES;
