@@ -168,6 +168,9 @@ __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) 
     // operations of one wave complete in order, so a slab's reads finish
     // before the next slab overwrites it.
     XItem<XDT> x0[NI], x1[NI], x2[NI];  // x1, x2: BF only
+    // weights WD slabs ahead (WD + 1 register sets); four row tiles a wave
+    // keep one slab ahead in two sets, for fewer registers
+    constexpr int WD = (!BF && RT >= 4) ? 1 : 2;
     WSet w0, w1, w2;
     if constexpr (BF) {
         load_x(s_beg, x0);
@@ -177,7 +180,7 @@ __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) 
     } else if (s_beg < s_end) {
         load_x(s_beg, x0);
         load_w(s_beg, w0);
-        if (s_beg + 1 < s_end) load_w(s_beg + 1, w1);
+        if (WD == 2 && s_beg + 1 < s_end) load_w(s_beg + 1, w1);
     }
     auto step = [&](int s, const WSet& wc, WSet& wnext2, XItem<XDT>* xc, XItem<XDT>* xnext2) {
         const bool live = !BF || s < s_end;
@@ -188,7 +191,7 @@ __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) 
             load_w(s + 2, wnext2);
         } else {
             if (s + 1 < s_end) load_x(s + 1, xc);
-            if (s + 2 < s_end) load_w(s + 2, wnext2);
+            if (s + WD < s_end) load_w(s + WD, wnext2);
         }
 #pragma unroll
         for (int f = 0; f < NF; f++) {
@@ -232,6 +235,12 @@ __global__ __launch_bounds__(kTokThreads) void qgemm_tok_int4_kernel(TokArgs a) 
             }
         }
     };
+    if constexpr (!BF && WD == 1) {  // two sets: pairs of slabs
+        for (int s = s_beg; s < s_end; s += 2) {
+            step(s, w0, w1, x0, x0);
+            if (s + 1 < s_end) step(s + 1, w1, w0, x0, x0);
+        }
+    } else
     for (int s = s_beg; s < s_end; s += 3) {
         if constexpr (BF) {
             step(s, w0, w2, x0, x2);
