@@ -60,7 +60,8 @@ TQ_DEV th8 tok_b8(uint32_t w) {
     return __builtin_bit_cast(th8, v);
 }
 
-// TM tokens per workgroup (grid.z walks the token tiles); the workgroup owns
+// TM tokens per workgroup (blockIdx.x walks row blocks and token tiles,
+// blockIdx.y the problems); the workgroup owns
 // RT 16-row tiles and its 4 waves split K in quarters, each wave staging its
 // own activation slabs (no barrier in the main loop), with a deterministic
 // reduction of the 4 partial sums through LDS at the end.  FW code words (32
@@ -374,14 +375,12 @@ int run_tok_int4(const titan_qweight* Ws, const void* const* Xs, const int64_t* 
     }
     const int gs = Ws[0].group_size;
     const int fw = gs >= 128 ? 4 : gs / 32;
-    // token tile and row tiles per wave (measured on the 8B layer): one
-    // 16-token tile with two row tiles up to 16 tokens; 16-token tiles with
-    // four row tiles up to 64 tokens (32-token tiles, or two row tiles,
-    // measured 1-8% slower at 24 and 32 tokens); 64-token tiles beyond
-    constexpr int kT16Max = 64;  // largest M served by 16-token tiles
+    // 16-token tiles (measured on the 8B layer): two row tiles a wave up to 16
+    // tokens, four beyond (32-token tiles, or two row tiles, measured 1-8%
+    // slower at 24 and 32 tokens; 64-token tiles 10-36% slower from 80 to
+    // 512 tokens)
     if (M <= 16) tq::launch_tok_f<16, 2>(a, maxrows, fw, xdt, ydt, st);
-    else if (M <= kT16Max) tq::launch_tok_f<16, 4>(a, maxrows, fw, xdt, ydt, st);
-    else tq::launch_tok_f<64, 2>(a, maxrows, fw, xdt, ydt, st);
+    else tq::launch_tok_f<16, 4>(a, maxrows, fw, xdt, ydt, st);
     return launch_status();
 }
 
