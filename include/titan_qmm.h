@@ -137,9 +137,9 @@ int titan_qgemm_batched(const titan_qweight* Ws, const void* const* Xs, void* co
 /* The same products with the K (column) range of small problems split across
  * workgroups (no counterpart in the reference: its GEMV launches one block
  * per row, dequant.cu:227-240).  Used for the 256-column-chunk formats
- * (INT2, Q3_K) when the launch would otherwise hold fewer waves than the
- * chip needs (e.g. the 1024 x 8192 projections of a 70B layer), where it
- * measured faster; every other case runs exactly as titan_qgemm /
+ * (Q3_K; INT2 from two tokens) when the launch would otherwise hold fewer
+ * waves than the GPU has CUs (matrices of fewer than about 1024 rows), where
+ * it measured faster; every other case runs exactly as titan_qgemm /
  * titan_qgemm_batched.
  * `workspace` is a caller-owned device buffer of at least
  * titan_qgemm_workspace_bytes() bytes, 256-byte aligned, zero-filled once

@@ -28,9 +28,10 @@ def _call_noalloc(Ws, Xs, Ys):
 
 @pytest.mark.parametrize("fmt,gs", [("int2", 64), ("q3k", 256)])
 def test_noalloc_matches_workspace_entry_point(fmt, gs, rng):
-    # call 1: two 1024 x 8192 problems, 4 tokens (the K split engages);
-    # call 2: one smaller 512 x 4096 problem, 1 token
-    calls = [([(1024, 8192), (1024, 8192)], 4), ([(512, 4096)], 1)]
+    # call 1: two 256 x 8192 problems, 4 tokens; call 2: one smaller
+    # 128 x 4096 problem, 2 tokens (both launches hold fewer waves than CUs,
+    # so the K split engages in both)
+    calls = [([(256, 8192), (256, 8192)], 4), ([(128, 4096)], 2)]
     for shapes, M in calls:
         print(f"noalloc {fmt} shapes={shapes} M={M}", flush=True)
         ds = [make_weights(fmt, r, c, rng, gs=gs) for r, c in shapes]

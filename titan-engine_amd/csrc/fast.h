@@ -368,6 +368,9 @@ struct FxInt2 {
     // row tile (8192 x 28672 at four tokens 47.6-49.3 -> 45.2 us, 8192 x 8192
     // 17.4 -> 16.1 us; one token and small launches keep the wider split)
     static constexpr bool KS1_MULTI_PHASE = true;
+    // the cross-workgroup K split from two tokens on: at one token it
+    // measured no faster (128-512 x 8192: 6.6 -> 6.6-6.9 us)
+    static constexpr int XS_MIN_M = 2;
     static constexpr bool SB_CELL = LAYOUT == TITAN_LAYOUT_TILED;
     struct Off { uint32_t c, s, b; };
     struct Raw { uint32_t w[4], s[4], b[4]; uint4 q; };
@@ -669,6 +672,11 @@ struct FxQ4K {
     // waves, not four) measured 2-5% faster on the Llama-3-8B layer (31.7 ->
     // 30.5 us); INT4 measured slower with the same target
     static constexpr long long WAVES_TARGET_M1 = 1536;
+    // two to eight tokens: groups of two chunks (8B layer: 2 tokens 35.5-38.9
+    // -> 31.1-32.3 us, 4 tokens 45.3-46.6 -> 40.1-41.8 us, 28672 x 8192 at 4
+    // tokens 48.4-49.3 -> 43.0 us); one token about 1-2% slower and 16
+    // tokens 35% slower with them
+    static constexpr int U2_MIN_M = 2, U2_MAX_M = 8;
     struct Off { uint32_t c, h; };
     struct Raw { uint32_t w[4]; uint4 hdr; };
     // decode<GS>(w, raw, c, j) uses only the parity of c (which half block)
@@ -847,6 +855,11 @@ struct FxQ3K {
     // the Llama-3-8B layer at one token (40.8 -> 35.5-36.0 us) and on
     // 28672x8192 at four tokens (58.5 -> 51.9 us), the other shapes unchanged
     static constexpr long long WAVES_TARGET = 1536;
+    // every token count: groups of two chunks (8B layer: one token 31.9-32.1
+    // -> 29.9-30.1 us, 8 tokens 76.6-77.3 -> 73.6-73.7 us, 16 tokens 158.4
+    // -> 130.8-131.1 us, 2-4 tokens 2-3% faster; 1024 x 8192 one token 9.6
+    // -> 9.0 us)
+    static constexpr int U2_MIN_M = 1, U2_MAX_M = 16;
     // the EXACT kernel of this fold holds ~290 VGPRs against ~155 (one wave
     // per SIMD instead of three): Q3_K keeps the general kernel
     static constexpr bool NO_EXACT = true;

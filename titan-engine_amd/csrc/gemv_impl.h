@@ -54,6 +54,16 @@ constexpr bool allow_exact() {
 #define TQ_GEMV_WAVES_TARGET 2048
 #endif
 template <class F, class = void>
+struct has_xs_min_m : std::false_type {};
+template <class F>
+struct has_xs_min_m<F, std::void_t<decltype(F::XS_MIN_M)>> : std::true_type {};
+// fewest tokens for which a caller workspace splits K across workgroups
+template <class F>
+constexpr int xs_min_m() {
+    if constexpr (has_xs_min_m<F>::value) return F::XS_MIN_M;
+    else return 1;
+}
+template <class F, class = void>
 struct has_waves_target_m1 : std::false_type {};
 template <class F>
 struct has_waves_target_m1<F, std::void_t<decltype(F::WAVES_TARGET_M1)>> : std::true_type {};
@@ -266,9 +276,21 @@ TQ_DEV void stage_f16(_Float16* xh, float* s16, int pc, const void* x, int64_t l
 }
 
 // chunks per load group (a larger group needs a proportionally larger
-// activation stage, which costs more in occupancy than it gains)
+// activation stage, which costs more in occupancy than it gains); a format
+// that sets U2_MIN_M / U2_MAX_M folds U2_MIN_M..U2_MAX_M tokens on the matrix
+// cores in groups of two chunks (half the registers in flight a wave, so
+// more waves a SIMD)
+template <class F, class = void>
+struct has_u2 : std::false_type {};
+template <class F>
+struct has_u2<F, std::void_t<decltype(F::U2_MIN_M), decltype(F::U2_MAX_M)>> : std::true_type {};
 template <class F, int M, int MODE>
-constexpr int gemv_u() { return TQ_GEMV_U; }
+constexpr int gemv_u() {
+    if constexpr (MODE == kModeMfma && has_u2<F>::value)
+        return M >= F::U2_MIN_M && M <= F::U2_MAX_M ? 2 : TQ_GEMV_U;
+    else
+        return TQ_GEMV_U;
+}
 
 template <class F, class = void>
 struct has_half_from_u : std::false_type {};
@@ -899,22 +921,21 @@ void launch_mode(const GemvArgs& args, int, hipStream_t st) {
     // workgroups too.  Each wave keeps at least one whole group of U chunks;
     // the problems' waves keep one workgroup per row tile group within the K
     // split (ks = 0: four row tiles a workgroup, the smallest activation stage).
-    // Measured (rocprof, 1024 x 8192): Q3_K M = 1 11.2 -> 10.0 us, INT2 M = 4
-    // 13.8 -> 11.7 us; for the 128-column-chunk formats (INT4, Q4_K 4096^2:
-    // 8.2 -> 10.2 us) the partials' round trips cost more than the extra
-    // waves gain, so they keep the single-workgroup tiles.
+    // For the 128-column-chunk formats (INT4, Q4_K 4096^2: 8.2 -> 10.2 us)
+    // the partials' round trips cost more than the extra waves gain, so they
+    // keep the single-workgroup tiles.
     // The split aims for the same wave count as the in-workgroup split (the
     // smaller of TQ_GEMV_XS_WAVES and the format's target) and engages only
-    // for launches of at most half that many waves: one the format already
-    // counts as full (Q3_K / INT2 28672 x 8192 at 1792 waves against a 1536
-    // target), or close to full, keeps its single-workgroup tiles and the
-    // tail split below, which needs no partials.
-    if (a.ws && F::CHUNK_COLS > 128) {
+    // for launches of fewer waves than CUs: Q3_K 256 x 28672 one token
+    // 24.0 -> 13.2 us, 128 x 8192 8.9 -> 7.2 us, INT2 256 x 8192 four tokens
+    // 12.2 -> 11.2 us; at 256 to 768 waves (1024 x 8192, 4096^2) it measured
+    // up to 20% slower (Q3_K 4096^2 four tokens 11.6 -> 14.1 us).
+    if (a.ws && F::CHUNK_COLS > 128 && M >= xs_min_m<F>()) {
         constexpr int U = gemv_u<F, M, MODE>();
         constexpr long long xs_waves = wt < TQ_GEMV_XS_WAVES ? wt : TQ_GEMV_XS_WAVES;
         long long waves = 0;
         for (int i = 0; i < a.n; i++) waves += (long long)a.p[i].ntiles << a.p[i].ks_log;
-        if (2 * waves <= xs_waves) {
+        if (waves < 256) {
             int xs = 0;
             long long w0 = 0;
             for (int i = 0; i < a.n; i++) w0 += a.p[i].ntiles;
