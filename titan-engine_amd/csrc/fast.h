@@ -149,6 +149,11 @@ struct FxNib {
     // one token: 1536 waves aimed for (the 8B layer's 14336-column rows split
     // over two waves, not four): 22.6 -> 21.2 us on the layer
     static constexpr long long WAVES_TARGET_M1 = IS_FP4 ? 2048 : 1536;  // FP4: the default
+    // FP4, five to eight tokens: groups of two chunks (4096 x 14336 53.3 ->
+    // 49.9 us, 14336 x 4096 unchanged; one to four tokens gain on one shape
+    // and lose on the other); INT4 never (U2_MIN_M above every token count:
+    // its scale cells span four chunks)
+    static constexpr int U2_MIN_M = IS_FP4 ? 8 : 64, U2_MAX_M = 8;
     // tiled INT4: the scales come in 16-byte cells, one load per GS chunks
     static constexpr bool SB_CELL = LAYOUT == TITAN_LAYOUT_TILED && !IS_FP4;
     struct Off { uint32_t c, s, b; };
@@ -575,6 +580,9 @@ template <int LAYOUT>
 struct FxNvfp4 {
     static constexpr int FMT = TITAN_NVFP4, CHUNK_COLS = 128;
     static constexpr bool HAS_MFMA = false, PIPE = true;
+    // five to eight tokens: groups of two chunks (4096 x 14336 56.2 -> 51.5
+    // us, 14336 x 4096 unchanged; one and four tokens lose on one shape)
+    static constexpr int U2_MIN_M = 8, U2_MAX_M = 8;
     struct Off { uint32_t c, s; };
     struct Raw { uint32_t w[4]; uint32_t s0, s1; };
     struct Dec { float s[4]; };
@@ -1082,6 +1090,10 @@ template <int LAYOUT>
 struct FxFp8 {
     static constexpr int FMT = TITAN_FP8_E4M3, CHUNK_COLS = 64;
     static constexpr bool HAS_MFMA = false, PIPE = true;
+    // three or four tokens: groups of two chunks (4096 x 14336 35.3-35.5 ->
+    // 28.9-29.0 us, 14336 x 4096 24.0 -> 23.5 us; one token 20% and eight
+    // tokens 10% slower on one shape)
+    static constexpr int U2_MIN_M = 4, U2_MAX_M = 4;
     struct Off { uint32_t c; };
     struct Raw { uint32_t w[4]; };
     struct Dec {};

@@ -277,16 +277,16 @@ TQ_DEV void stage_f16(_Float16* xh, float* s16, int pc, const void* x, int64_t l
 
 // chunks per load group (a larger group needs a proportionally larger
 // activation stage, which costs more in occupancy than it gains); a format
-// that sets U2_MIN_M / U2_MAX_M folds U2_MIN_M..U2_MAX_M tokens on the matrix
-// cores in groups of two chunks (half the registers in flight a wave, so
-// more waves a SIMD)
+// that sets U2_MIN_M / U2_MAX_M folds U2_MIN_M..U2_MAX_M tokens of fp16
+// activations (its matrix-core or dot2 fold) in groups of two chunks (half
+// the registers in flight a wave, so more waves a SIMD)
 template <class F, class = void>
 struct has_u2 : std::false_type {};
 template <class F>
 struct has_u2<F, std::void_t<decltype(F::U2_MIN_M), decltype(F::U2_MAX_M)>> : std::true_type {};
 template <class F, int M, int MODE>
 constexpr int gemv_u() {
-    if constexpr (MODE == kModeMfma && has_u2<F>::value)
+    if constexpr (MODE == (F::HAS_MFMA ? kModeMfma : kModeDot2) && has_u2<F>::value)
         return M >= F::U2_MIN_M && M <= F::U2_MAX_M ? 2 : TQ_GEMV_U;
     else
         return TQ_GEMV_U;
