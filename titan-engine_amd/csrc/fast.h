@@ -147,8 +147,10 @@ struct FxNib {
     static constexpr int CHUNK_COLS = 128;
     static constexpr bool HAS_MFMA = !IS_FP4, PIPE = true;
     // one token: 1536 waves aimed for (the 8B layer's 14336-column rows split
-    // over two waves, not four): 22.6 -> 21.2 us on the layer
-    static constexpr long long WAVES_TARGET_M1 = IS_FP4 ? 2048 : 1536;  // FP4: the default
+    // over two waves, not four): 22.6 -> 21.2 us on the layer; FP4 14336 x
+    // 4096 13.4 -> 12.3 us (4096 x 14336 unchanged; several tokens measured
+    // slower with it)
+    static constexpr long long WAVES_TARGET_M1 = 1536;
     // FP4, five to eight tokens: groups of two chunks (4096 x 14336 53.3 ->
     // 49.9 us, 14336 x 4096 unchanged; one to four tokens gain on one shape
     // and lose on the other); INT4 never (U2_MIN_M above every token count:
@@ -580,6 +582,9 @@ template <int LAYOUT>
 struct FxNvfp4 {
     static constexpr int FMT = TITAN_NVFP4, CHUNK_COLS = 128;
     static constexpr bool HAS_MFMA = false, PIPE = true;
+    // one token: 1536 waves aimed for (14336 x 4096 16.15 -> 15.4 us,
+    // 4096 x 14336 unchanged; four and eight tokens slower with it)
+    static constexpr long long WAVES_TARGET_M1 = 1536;
     // five to eight tokens: groups of two chunks (4096 x 14336 56.2 -> 51.5
     // us, 14336 x 4096 unchanged; one and four tokens lose on one shape)
     static constexpr int U2_MIN_M = 8, U2_MAX_M = 8;
@@ -1090,6 +1095,9 @@ template <int LAYOUT>
 struct FxFp8 {
     static constexpr int FMT = TITAN_FP8_E4M3, CHUNK_COLS = 64;
     static constexpr bool HAS_MFMA = false, PIPE = true;
+    // one token: 1536 waves aimed for (14336 x 4096 14.1-14.3 -> 13.0-13.3
+    // us, 4096 x 14336 unchanged; eight tokens slower with it)
+    static constexpr long long WAVES_TARGET_M1 = 1536;
     // three or four tokens: groups of two chunks (4096 x 14336 35.3-35.5 ->
     // 28.9-29.0 us, 14336 x 4096 24.0 -> 23.5 us; one token 20% and eight
     // tokens 10% slower on one shape)
