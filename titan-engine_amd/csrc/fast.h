@@ -864,10 +864,13 @@ struct FxQ4K {
 template <int LAYOUT>
 struct FxQ3K {
     static constexpr int FMT = TITAN_Q3_K, CHUNK_COLS = 256;
-    // fewer, longer waves than the default 2048: measured 11-13% faster on
-    // the Llama-3-8B layer at one token (40.8 -> 35.5-36.0 us) and on
-    // 28672x8192 at four tokens (58.5 -> 51.9 us), the other shapes unchanged
-    static constexpr long long WAVES_TARGET = 1536;
+    // 2048 waves aimed for (the default).  With four-chunk groups 1536
+    // measured 11-13% faster (8B layer one token 40.8 -> 35.5-36.0 us);
+    // with two-chunk groups 2048 is: 28672 x 8192 one token 32.6-34.6 ->
+    // 30.5-30.6 us, 8B layer two tokens 42.4-42.7 -> 39.9-41.1 us, the layer
+    // at one token within 1 us either way, 8192 x 28672 one token 1-2%
+    // slower in one pair
+    static constexpr long long WAVES_TARGET = 2048;
     // every token count: groups of two chunks (8B layer: one token 31.9-32.1
     // -> 29.9-30.1 us, 8 tokens 76.6-77.3 -> 73.6-73.7 us, 16 tokens 158.4
     // -> 130.8-131.1 us, 2-4 tokens 2-3% faster; 1024 x 8192 one token 9.6
